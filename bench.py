@@ -1,0 +1,364 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X HIP backend's hot path (one GPU).
+
+Headline (`value`): fused Q4_0 dequant-matvec throughput in GB/s on the decode
+shape of the benchmark configuration 2: W = Q4_0 [K=4096, M=14336], x = F32
+[4096, 1], y = F32 [14336, 1]. One step = one fused kernel launch over one
+batch. Algorithmic bytes per step = W blocks + x + y = 33,103,872 B.
+
+The same run also measures, each against its roofline (`extra`):
+  - bulk dequant of all five formats on 4096 x 11008 (configuration 1), GB/s;
+  - the fused kernel for Q4_0/Q5_0 at N = 1 and 16 (configuration 2);
+  - the F32 mul_mat forward + both backward products of a 4096x4096 linear
+    layer over 512 tokens (configuration 3) and the batched broadcast product
+    with a permuted src1 (configuration 4), TFLOP/s on the FP32 MFMA roofline.
+
+Timing: steps are enqueued on one stream and captured into a HIP graph (host
+launch overhead stays out of the timed region); HIP events on that stream
+bracket the K timed replays. Inputs rotate over buffer sets totalling more
+than 512 MB so the 256 MB Infinity Cache cannot hold them between steps.
+
+cpu_baseline: the reference CPU path (dequantize the whole weight, then the
+serial mul_mat loop) restated in oracle/ and run single-threaded on this
+host's cores for the headline workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "train.cpp_amd"
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+FP32_MFMA_PEAK_TFS = 157.3   # MI355X dense FP32 matrix, TFLOP/s
+METRIC = "Q4_0 dequant-matvec GB/s (% HBM peak); F32 mul_mat TFLOP/s (% MFMA peak)"
+
+
+def load_pkg():
+    spec = importlib.util.spec_from_file_location("traincpp_amd", PKG / "__init__.py",
+                                                  submodule_search_locations=[str(PKG)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["traincpp_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+# ---------------------------------------------------------------- HIP runtime (events, streams, graphs)
+
+class Hip:
+    def __init__(self):
+        self.rt = C.CDLL("libamdhip64.so")
+        V, P = C.c_void_p, C.POINTER(C.c_void_p)
+        for name, args in {
+            "hipStreamCreate": [P], "hipStreamDestroy": [V], "hipStreamSynchronize": [V],
+            "hipEventCreate": [P], "hipEventRecord": [V, V], "hipEventSynchronize": [V],
+            "hipEventElapsedTime": [C.POINTER(C.c_float), V, V], "hipEventDestroy": [V],
+            "hipStreamBeginCapture": [V, C.c_int], "hipStreamEndCapture": [V, P],
+            "hipGraphInstantiate": [P, V, V, V, C.c_size_t], "hipGraphLaunch": [V, V],
+            "hipGraphExecDestroy": [V], "hipGraphDestroy": [V], "hipDeviceSynchronize": [],
+        }.items():
+            fn = getattr(self.rt, name)
+            fn.argtypes = args
+            fn.restype = C.c_int
+
+    def ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with hipError_t {rc}")
+
+    def stream(self):
+        s = C.c_void_p()
+        self.ok(self.rt.hipStreamCreate(C.byref(s)), "hipStreamCreate")
+        return s.value
+
+    def event(self):
+        e = C.c_void_p()
+        self.ok(self.rt.hipEventCreate(C.byref(e)), "hipEventCreate")
+        return e.value
+
+    def elapsed_ms(self, a, b):
+        f = C.c_float()
+        self.ok(self.rt.hipEventElapsedTime(C.byref(f), a, b), "hipEventElapsedTime")
+        return f.value
+
+
+class Timer:
+    """Times `steps` calls of fn(i) enqueued on one stream, as a HIP graph replay
+    when capture works (falls back to plain stream launches)."""
+
+    def __init__(self, hip: Hip, use_graph: bool = True):
+        self.hip = hip
+        self.stream = hip.stream()
+        self.e0, self.e1 = hip.event(), hip.event()
+        self.use_graph = use_graph
+
+    def run(self, fn, steps: int, warmup: int) -> tuple[float, str]:
+        hip, rt, s = self.hip, self.hip.rt, self.stream
+        for i in range(warmup):
+            fn(i, s)
+        hip.ok(rt.hipStreamSynchronize(s), "sync")
+        mode = "stream"
+        exec_ = None
+        if self.use_graph:
+            graph, gexec = C.c_void_p(), C.c_void_p()
+            try:
+                hip.ok(rt.hipStreamBeginCapture(s, 2), "hipStreamBeginCapture")  # relaxed mode
+                for i in range(steps):
+                    fn(warmup + i, s)
+                hip.ok(rt.hipStreamEndCapture(s, C.byref(graph)), "hipStreamEndCapture")
+                hip.ok(rt.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0), "hipGraphInstantiate")
+                exec_ = gexec.value
+                hip.ok(rt.hipGraphLaunch(exec_, s), "hipGraphLaunch")  # one untimed replay
+                hip.ok(rt.hipStreamSynchronize(s), "sync")
+                mode = "graph"
+            except RuntimeError:
+                exec_ = None
+        hip.ok(rt.hipDeviceSynchronize(), "sync")
+        hip.ok(rt.hipEventRecord(self.e0, s), "record")
+        if exec_ is not None:
+            hip.ok(rt.hipGraphLaunch(exec_, s), "hipGraphLaunch")
+        else:
+            for i in range(steps):
+                fn(warmup + i, s)
+        hip.ok(rt.hipEventRecord(self.e1, s), "record")
+        hip.ok(rt.hipEventSynchronize(self.e1), "sync")
+        hip.ok(rt.hipDeviceSynchronize(), "sync")
+        ms = hip.elapsed_ms(self.e0, self.e1)
+        if exec_ is not None:
+            rt.hipGraphExecDestroy(exec_)
+        return ms / steps, mode
+
+
+# ---------------------------------------------------------------- workloads
+
+def rotation_count(bytes_per_set: int, floor: int = 3, target: int = 512 << 20) -> int:
+    return max(floor, -(-target // max(bytes_per_set, 1)) + 1)
+
+
+def qmatvec_case(H, synth, timer, t, K, M, N, steps, warmup):
+    blk = synth.block_bytes(synth.quant_blocks(t, K * M // 32, synth.config_seed(2, t)))
+    x = synth.normal(synth.config_seed(2, 100 + N), K * N)
+    alg_bytes = blk.nbytes + x.nbytes + M * N * 4
+    sets = rotation_count(alg_bytes)
+    ws = [H.DeviceBuffer(blk.nbytes).upload(blk) for _ in range(sets)]
+    xs = [H.DeviceBuffer(x.nbytes).upload(x) for _ in range(sets)]
+    ys = [H.DeviceBuffer(M * N * 4) for _ in range(sets)]
+    nb1_w = (K // 32) * H.BLOCK_BYTES[t]
+
+    def step(i, s):
+        j = i % sets
+        H.qmatvec(t, ws[j].ptr, K, M, nb1_w, xs[j].ptr, N, K * 4, ys[j].ptr, M * 4, s)
+
+    ms, mode = timer.run(step, steps, warmup)
+    for b in ws + xs + ys:
+        b.free()
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    flops = 2.0 * K * M * N
+    return {"ms": ms, "bytes": alg_bytes, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS,
+            "TFLOP/s": flops / (ms * 1e-3) / 1e12, "sets": sets, "timing": mode}, blk, x
+
+
+def dequant_case(H, synth, timer, t, n_blocks, steps, warmup):
+    blk = synth.block_bytes(synth.quant_blocks(t, n_blocks, synth.config_seed(1, t)))
+    alg_bytes = blk.nbytes + n_blocks * 32 * 4
+    sets = rotation_count(alg_bytes)
+    srcs = [H.DeviceBuffer(blk.nbytes).upload(blk) for _ in range(sets)]
+    dsts = [H.DeviceBuffer(n_blocks * 128) for _ in range(sets)]
+
+    def step(i, s):
+        j = i % sets
+        H.dequant(t, srcs[j].ptr, n_blocks, dsts[j].ptr, s)
+
+    ms, mode = timer.run(step, steps, warmup)
+    for b in srcs + dsts:
+        b.free()
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    return {"ms": ms, "bytes": alg_bytes, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS, "sets": sets,
+            "timing": mode}
+
+
+def mul_mat_config3(H, synth, timer, steps, warmup):
+    """Y = mul_mat(W, X); dX = mul_mat(transpose(W), dY); dW^T = mul_mat(transpose(dY), transpose(X))."""
+    K = M = 4096
+    T = 512
+    n = K * M // 32
+    q = synth.block_bytes(synth.quant_blocks(7, n, synth.config_seed(3, 0)))  # Q5_1 weights
+    qd = H.DeviceBuffer(q.nbytes).upload(q)
+    Wd = H.DeviceBuffer(K * M * 4)
+    H.dequant(7, qd.ptr, n, Wd.ptr)  # W is the GPU dequant of the Q5_1 blocks
+    H.sync()
+    Xd = H.DeviceBuffer(K * T * 4).upload(synth.normal(synth.config_seed(3, 1), K * T))
+    dYd = H.DeviceBuffer(K * T * 4).upload(synth.normal(synth.config_seed(3, 2), K * T, 0.0, 1e-2))
+    Yd = H.DeviceBuffer(M * T * 4)
+    dXd = H.DeviceBuffer(K * T * 4)
+    dWd = H.DeviceBuffer(K * M * 4)
+    f4 = 4
+    W = H.tensor(Wd.ptr, [K, M, 1, 1], [f4, K * f4, K * M * f4, K * M * f4])
+    Wt = H.tensor(Wd.ptr, [M, K, 1, 1], [K * f4, f4, K * M * f4, K * M * f4])
+    X = H.tensor(Xd.ptr, [K, T, 1, 1], [f4, K * f4, K * T * f4, K * T * f4])
+    Xt = H.tensor(Xd.ptr, [T, K, 1, 1], [K * f4, f4, K * T * f4, K * T * f4])
+    dY = H.tensor(dYd.ptr, [M, T, 1, 1], [f4, M * f4, M * T * f4, M * T * f4])
+    dYt = H.tensor(dYd.ptr, [T, M, 1, 1], [M * f4, f4, M * T * f4, M * T * f4])
+    Y = H.tensor(Yd.ptr, [M, T, 1, 1], H.contiguous_nb([M, T, 1, 1]))
+    dX = H.tensor(dXd.ptr, [K, T, 1, 1], H.contiguous_nb([K, T, 1, 1]))
+    dWt = H.tensor(dWd.ptr, [M, K, 1, 1], H.contiguous_nb([M, K, 1, 1]))
+    prods = {"fwd Y=W.X": (W, X, Y), "bwd dX=W^T.dY": (Wt, dY, dX), "bwd dW^T=dY^T.X^T": (dYt, Xt, dWt)}
+    out = {}
+    total_ms = 0.0
+    for name, (a, b, d) in prods.items():
+        ms, mode = timer.run(lambda i, s, a=a, b=b, d=d: H.mul_mat_f32(a, b, d, s), steps, warmup)
+        fl = 2.0 * K * M * T
+        out[name] = {"ms": ms, "TFLOP/s": fl / (ms * 1e-3) / 1e12,
+                     "frac_mfma": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFS, "timing": mode}
+        total_ms += ms
+    fl = 3 * 2.0 * K * M * T
+    out["fwd+bwd"] = {"ms": total_ms, "TFLOP/s": fl / (total_ms * 1e-3) / 1e12,
+                      "frac_mfma": fl / (total_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFS}
+    for b in (qd, Wd, Xd, dYd, Yd, dXd, dWd):
+        b.free()
+    return out
+
+
+def mul_mat_config4(H, synth, timer, steps, warmup):
+    A = synth.normal(synth.config_seed(4, 0), 128 * 1024 * 8 * 4)
+    B = synth.normal(synth.config_seed(4, 1), 128 * 32 * 512 * 4)
+    Ad = H.DeviceBuffer(A.nbytes).upload(A)
+    Bd = H.DeviceBuffer(B.nbytes).upload(B)
+    Dd = H.DeviceBuffer(1024 * 512 * 32 * 4 * 4)
+    a = H.tensor(Ad.ptr, [128, 1024, 8, 4], H.contiguous_nb([128, 1024, 8, 4]))
+    b = H.tensor(Bd.ptr, [128, 512, 32, 4], [4, 16384, 512, 8388608])  # permute(base[128,32,512,4],0,2,1,3)
+    d = H.tensor(Dd.ptr, [1024, 512, 32, 4], H.contiguous_nb([1024, 512, 32, 4]))
+    ms, mode = timer.run(lambda i, s: H.mul_mat_f32(a, b, d, s), steps, warmup)
+    fl = 2.0 * 128 * 1024 * 512 * 128
+    for x in (Ad, Bd, Dd):
+        x.free()
+    return {"ms": ms, "TFLOP/s": fl / (ms * 1e-3) / 1e12, "frac_mfma": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFS,
+            "timing": mode}
+
+
+# ---------------------------------------------------------------- CPU baseline (reference path, oracle/)
+
+def cpu_baseline(blk: np.ndarray, x: np.ndarray, K: int, M: int, budget_s: float):
+    """The reference path for the headline workload on this host: dequantize the
+    whole Q4_0 weight (gguf_tensor_to_f32) then the serial mul_mat loop, one thread."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+    lib = O.oracle()
+    wf = np.empty(K * M, dtype=np.float32)
+    xv = x.reshape(1, 1, 1, K)
+    y = np.empty((1, 1, 1, M), dtype=np.float32)
+    ane, anb = [K, M, 1, 1], [4, 4 * K, 4 * K * M, 4 * K * M]
+    bne, bnb = [K, 1, 1, 1], [4, 4 * K, 4 * K, 4 * K]
+    dne, dnb = [M, 1, 1, 1], [4, 4 * M, 4 * M, 4 * M]
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        assert lib.orc_dequant(2, blk.ctypes.data, K * M // 32, wf.ctypes.data, 1) == 0
+        assert lib.orc_mul_mat(wf.ctypes.data, O.NE(*ane), O.NB(*anb), xv.ctypes.data, O.NE(*bne), O.NB(*bnb),
+                               y.ctypes.data, O.NE(*dne), O.NB(*dnb), 1) == 0
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    alg = blk.nbytes + x.nbytes + M * 4
+    return {"value": alg / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"full headline workload (Q4_0 W[4096,14336] dequant to F32 + mul_mat with x[4096,1]), "
+                      f"{reps} repetitions, {dt * 1e3:.1f} ms each, oracle/oracle.cpp -O3 -ffp-contract=off, 1 thread"}
+
+
+def read_traffic():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor)."""
+    p = ROOT / "profiles" / "qmatvec_q4_0_n1_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return float(json.loads(p.read_text())["traffic_bytes_per_launch"])
+    except Exception:
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this backend is measured on one GPU; multi-GPU runs are not part of this "
+                                   "build (the sharding design is in DESIGN.md)", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    pkg = load_pkg()
+    from traincpp_amd import hip as H
+    from traincpp_amd import synth
+    props = H.init(0)
+    hip = Hip()
+    timer = Timer(hip, use_graph=not args.no_graph)
+    K, M = 4096, 14336
+
+    t_wall = time.perf_counter()
+    head, blk, x = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 1, args.steps, args.warmup)
+    wall = time.perf_counter() - t_wall
+    traffic = read_traffic()
+    roofline = {"bound": "hbm", "achieved": head["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": head["GB/s"] / HBM_PEAK_GBS, "traffic": traffic,
+                "kernel": "k_qmatvec<Q4_0> (train.cpp_amd/csrc/hip/qmatvec.hip)",
+                "algorithmic_bytes_per_launch": head["bytes"]}
+
+    extra = {"device": f"{props.name.decode()} {props.arch.decode()} CUs={props.compute_units}"}
+    if not args.headline_only:
+        s, w = max(20, args.steps // 2), max(5, args.warmup // 2)
+        extra["qmatvec"] = {}
+        for name, t in (("q4_0", H.TYPE_Q4_0), ("q5_0", H.TYPE_Q5_0)):
+            for N in (1, 16):
+                if name == "q4_0" and N == 1:
+                    r = head
+                else:
+                    r, _, _ = qmatvec_case(H, synth, timer, t, K, M, N, s, w)
+                extra["qmatvec"][f"{name} N={N}"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+        extra["dequant_4096x11008"] = {}
+        for name, t in H.QUANT_TYPES.items():
+            r = dequant_case(H, synth, timer, t, 4096 * 11008 // 32, s, w)
+            extra["dequant_4096x11008"][name] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+        extra["mul_mat_cfg3_linear_4096x4096x512"] = mul_mat_config3(H, synth, timer, max(10, s // 4), 3)
+        extra["mul_mat_cfg4_batched_permuted"] = mul_mat_config4(H, synth, timer, max(10, s // 4), 3)
+
+    cpu = cpu_baseline(blk, x, K, M, args.cpu_budget)
+    extra["cpu_vs_gpu_speedup"] = head["GB/s"] / cpu["value"]
+
+    line = {
+        "metric": METRIC,
+        "value": round(head["GB/s"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded splitmix64: Q4_0 blocks with d~U[2e-4,1e-3] fp16, nibbles U{0..15}; x~N(0,1))",
+        "config": {"workload": "cfg2 decode: fused Q4_0 dequant-matvec, W[K=4096,M=14336] x F32 x[4096,1]",
+                   "K": K, "M": M, "N": 1, "rotating_sets": head["sets"], "timing": head["timing"],
+                   "wall_s_headline": round(wall, 3)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,129 @@
+// extern "C" shim over the REFERENCE library's public API, compiled together
+// with the reference's own sources (under /root/reference, never copied) into
+// oracle/_ref/libtrc_ref.so by oracle/Makefile. TEST INFRASTRUCTURE ONLY: it lets
+// the CPU tests check the oracle restatement (oracle.cpp) against the code it
+// restates. Nothing in the product loads it.
+//
+// Entry points go through the same public calls a traincpp user makes:
+//   ref_dequant   -> gguf_open + gguf_tensor_to_f32   (src/io/trc_gguf.cpp:748,966)
+//   ref_mul_mat   -> permute views + mul_mat + CPU Device::graph_compute
+//                    (src/ops/trc_ops.cpp:366, src/backends/cpu/trc_cpu_ops.cpp:182)
+//   ref_fp16_*    -> core/trc_float.h:23-63
+//   ref_rng_*     -> src/core/trc_rng.cpp:38-68
+#include "traincpp/traincpp.h"
+#include "core/trc_float.h"
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+using namespace traincpp;
+
+namespace {
+
+void put(std::vector<uint8_t>& v, const void* p, size_t n) {
+    const uint8_t* b = (const uint8_t*) p;
+    v.insert(v.end(), b, b + n);
+}
+
+template <typename T>
+void put_pod(std::vector<uint8_t>& v, T x) {
+    put(v, &x, sizeof(x));
+}
+
+void pad32(std::vector<uint8_t>& v) {
+    while (v.size() % 32 != 0) v.push_back(0);
+}
+
+}  // namespace
+
+extern "C" {
+
+float ref_fp16_to_fp32(uint16_t h) { return fp16_to_fp32(h); }
+uint16_t ref_fp32_to_fp16(float f) { return fp32_to_fp16(f); }
+
+uint64_t ref_rng_next_u64(uint64_t* state) {
+    Rng r;
+    r.state = *state;
+    const uint64_t v = rng_next_u64(&r);
+    *state = r.state;
+    return v;
+}
+
+float ref_rng_uniform01(uint64_t* state) {
+    Rng r;
+    r.state = *state;
+    const float v = rng_uniform01(&r);
+    *state = r.state;
+    return v;
+}
+
+float ref_rng_normal(uint64_t* state, float mean, float stddev) {
+    Rng r;
+    r.state = *state;
+    const float v = rng_normal(&r, mean, stddev);
+    *state = r.state;
+    return v;
+}
+
+// Writes a one-tensor GGUF v3 file (tensor "w", 1-D, ne0 = 32 * n_blocks) holding
+// the given raw blocks, then reads it back through the reference reader.
+int ref_dequant(int type, const void* blocks, int64_t n_blocks, float* out, const char* tmp_path) {
+    const size_t bsz = type_size((Type) type);
+    if (bsz == 0 || n_blocks <= 0) return -1;
+    std::vector<uint8_t> f;
+    put(f, "GGUF", 4);
+    put_pod<uint32_t>(f, 3);
+    put_pod<uint64_t>(f, 1);  // tensors
+    put_pod<uint64_t>(f, 0);  // kvs
+    put_pod<uint64_t>(f, 1);
+    f.push_back('w');
+    put_pod<uint32_t>(f, 1);
+    put_pod<int64_t>(f, 32 * n_blocks);
+    put_pod<uint32_t>(f, (uint32_t) type);
+    put_pod<uint64_t>(f, 0);
+    pad32(f);
+    put(f, blocks, bsz * (size_t) n_blocks);
+    pad32(f);
+    std::FILE* fp = std::fopen(tmp_path, "wb");
+    if (!fp) return -2;
+    const bool wrote = std::fwrite(f.data(), 1, f.size(), fp) == f.size();
+    std::fclose(fp);
+    if (!wrote) return -2;
+    GgufFile* g = gguf_open(tmp_path, true);
+    if (!g) return -3;
+    const bool ok = gguf_tensor_to_f32(g, "w", out, 32 * n_blocks);
+    gguf_close(g);
+    std::remove(tmp_path);
+    return ok ? 0 : -4;
+}
+
+// d = mul_mat(permute(A, pa), permute(B, pb)) on the reference CPU device.
+// A and B are contiguous F32 base tensors of shape a_ne / b_ne (ggml order);
+// pa / pb are the permute() axes. The result is copied out contiguously
+// (its shape is [A'.ne1, B'.ne1, B'.ne2, B'.ne3] for the permuted A', B').
+int ref_mul_mat(const float* a, const int64_t a_ne[4], const int pa[4],
+                const float* b, const int64_t b_ne[4], const int pb[4], float* out) {
+    Device* dev = device_cpu();
+    if (!dev) return -1;
+    Context* ctx = context_new(1 << 20);
+    Tensor* ta = new_tensor_4d(ctx, TYPE_F32, a_ne[0], a_ne[1], a_ne[2], a_ne[3]);
+    Tensor* tb = new_tensor_4d(ctx, TYPE_F32, b_ne[0], b_ne[1], b_ne[2], b_ne[3]);
+    Tensor* va = permute(ctx, ta, pa[0], pa[1], pa[2], pa[3]);
+    Tensor* vb = permute(ctx, tb, pb[0], pb[1], pb[2], pb[3]);
+    Tensor* r = mul_mat(ctx, va, vb);
+    Graph* g = graph_new(ctx);
+    graph_build_forward_expand(ctx, g, r);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    tensor_set(ta, a, 0, tensor_nbytes(ta));
+    tensor_set(tb, b, 0, tensor_nbytes(tb));
+    const bool ok = dev->graph_compute(g);
+    tensor_get(r, out, 0, tensor_nbytes(r));
+    buffer_free(buf);
+    graph_free(g);
+    context_free(ctx);
+    return ok ? 0 : -2;
+}
+
+}  // extern "C"

@@ -1,0 +1,162 @@
+"""ctypes access to the CPU checker for the tests.
+
+oracle/liboracle.so    the C++ restatement of the reference CPU path (oracle/oracle.cpp)
+oracle/_ref/libtrc_ref.so  the reference's own sources compiled with a small shim
+                           (oracle/ref_shim.cpp); present only where the reference
+                           checkout was available at build time.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_PATH = ROOT / "oracle" / "liboracle.so"
+REF_PATH = ROOT / "oracle" / "_ref" / "libtrc_ref.so"
+
+P, I, I64, F = C.c_void_p, C.c_int, C.c_int64, C.c_float
+NE = C.c_int64 * 4
+NB = C.c_size_t * 4
+AX = C.c_int * 4
+
+_orc = None
+_ref = None
+
+
+def oracle() -> C.CDLL:
+    global _orc
+    if _orc is None:
+        lib = C.CDLL(str(ORACLE_PATH))
+        lib.orc_fp16_to_fp32.argtypes = [C.c_uint16]
+        lib.orc_fp16_to_fp32.restype = F
+        lib.orc_fp32_to_fp16.argtypes = [F]
+        lib.orc_fp32_to_fp16.restype = C.c_uint16
+        lib.orc_fp16_to_fp32_n.argtypes = [P, P, I64]
+        lib.orc_fp32_to_fp16_n.argtypes = [P, P, I64]
+        lib.orc_block_bytes.argtypes = [I]
+        lib.orc_block_bytes.restype = I64
+        lib.orc_dequant.argtypes = [I, P, I64, P, I]
+        lib.orc_dequant.restype = I
+        lib.orc_mul_mat.argtypes = [P, NE, NB, P, NE, NB, P, NE, NB, I]
+        lib.orc_mul_mat.restype = I
+        lib.orc_mul_mat_cols.argtypes = [P, NE, NB, P, NE, NB, P, NE, NB, I64, I64, I]
+        lib.orc_mul_mat_cols.restype = I
+        lib.orc_rng_next_u64.argtypes = [C.POINTER(C.c_uint64)]
+        lib.orc_rng_next_u64.restype = C.c_uint64
+        lib.orc_rng_uniform01.argtypes = [C.POINTER(C.c_uint64)]
+        lib.orc_rng_uniform01.restype = F
+        lib.orc_rng_normal.argtypes = [C.POINTER(C.c_uint64), F, F]
+        lib.orc_rng_normal.restype = F
+        _orc = lib
+    return _orc
+
+
+def have_ref() -> bool:
+    return REF_PATH.exists()
+
+
+def ref() -> C.CDLL:
+    global _ref
+    if _ref is None:
+        lib = C.CDLL(str(REF_PATH))
+        lib.ref_fp16_to_fp32.argtypes = [C.c_uint16]
+        lib.ref_fp16_to_fp32.restype = F
+        lib.ref_fp32_to_fp16.argtypes = [F]
+        lib.ref_fp32_to_fp16.restype = C.c_uint16
+        lib.ref_dequant.argtypes = [I, P, I64, P, C.c_char_p]
+        lib.ref_dequant.restype = I
+        lib.ref_mul_mat.argtypes = [P, NE, AX, P, NE, AX, P]
+        lib.ref_mul_mat.restype = I
+        for n in ("ref_rng_next_u64", "ref_rng_uniform01"):
+            getattr(lib, n).argtypes = [C.POINTER(C.c_uint64)]
+        lib.ref_rng_next_u64.restype = C.c_uint64
+        lib.ref_rng_uniform01.restype = F
+        lib.ref_rng_normal.argtypes = [C.POINTER(C.c_uint64), F, F]
+        lib.ref_rng_normal.restype = F
+        _ref = lib
+    return _ref
+
+
+# ---------------------------------------------------------------- helpers
+
+def dequant(type_: int, blocks: np.ndarray, threads: int = 1) -> np.ndarray:
+    raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+    bb = oracle().orc_block_bytes(type_)
+    n = raw.size // bb
+    out = np.empty(n * 32, dtype=np.float32)
+    rc = oracle().orc_dequant(type_, raw.ctypes.data, n, out.ctypes.data, threads)
+    assert rc == 0
+    return out
+
+
+def ref_dequant(type_: int, blocks: np.ndarray, tmp_dir: str) -> np.ndarray:
+    raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+    bb = oracle().orc_block_bytes(type_)
+    n = raw.size // bb
+    out = np.empty(n * 32, dtype=np.float32)
+    path = os.path.join(tmp_dir, f"ref_{os.getpid()}_{type_}.gguf").encode()
+    rc = ref().ref_dequant(type_, raw.ctypes.data, n, out.ctypes.data, path)
+    assert rc == 0, rc
+    return out
+
+
+def view_meta(arr: np.ndarray):
+    """(ne, nb) in ggml order for a numpy array viewed as a ggml tensor (numpy
+    axes reversed: numpy shape (ne3, ne2, ne1, ne0))."""
+    assert arr.dtype == np.float32 and arr.ndim <= 4
+    shape = list(arr.shape)[::-1] + [1] * (4 - arr.ndim)
+    strides = list(arr.strides)[::-1]
+    nb = strides + [0] * (4 - arr.ndim)
+    # fill strides of the padded unit dims with the extent of the last real one
+    for i in range(arr.ndim, 4):
+        nb[i] = (nb[i - 1] * shape[i - 1]) if i > 0 else 4
+    return shape, nb
+
+
+def base_ptr_and_meta(arr: np.ndarray):
+    ne, nb = view_meta(arr)
+    return arr.__array_interface__["data"][0], ne, nb
+
+
+def mul_mat(a: np.ndarray, b: np.ndarray, threads: int = 1) -> np.ndarray:
+    """Oracle mul_mat of two (possibly strided) numpy views in ggml layout; returns
+    a contiguous numpy array of shape (ne3, ne2, ne1, ne0) of the result."""
+    pa, ane, anb = base_ptr_and_meta(a)
+    pb, bne, bnb = base_ptr_and_meta(b)
+    dne = [ane[1], bne[1], bne[2], bne[3]]
+    out = np.zeros((dne[3], dne[2], dne[1], dne[0]), dtype=np.float32)
+    _, _, dnb = base_ptr_and_meta(out)
+    rc = oracle().orc_mul_mat(pa, NE(*ane), NB(*anb), pb, NE(*bne), NB(*bnb), out.ctypes.data,
+                              NE(*dne), NB(*dnb), threads)
+    assert rc == 0
+    return out
+
+
+def ref_mul_mat(a_base: np.ndarray, pa, b_base: np.ndarray, pb) -> np.ndarray:
+    """Reference library mul_mat(permute(A, pa), permute(B, pb)) on its CPU device."""
+    a_base = np.ascontiguousarray(a_base, dtype=np.float32)
+    b_base = np.ascontiguousarray(b_base, dtype=np.float32)
+    ane = list(a_base.shape)[::-1] + [1] * (4 - a_base.ndim)
+    bne = list(b_base.shape)[::-1] + [1] * (4 - b_base.ndim)
+    ape = [0] * 4
+    bpe = [0] * 4
+    for i in range(4):  # the reference's permute(): ne_out[i] = ne_in[axes[i]] (src/core/trc_tensor.cpp:303-306)
+        ape[i] = ane[pa[i]]
+        bpe[i] = bne[pb[i]]
+    dne = [ape[1], bpe[1], bpe[2], bpe[3]]
+    out = np.zeros((dne[3], dne[2], dne[1], dne[0]), dtype=np.float32)
+    rc = ref().ref_mul_mat(a_base.ctypes.data, NE(*ane), AX(*pa), b_base.ctypes.data, NE(*bne), AX(*pb),
+                           out.ctypes.data)
+    assert rc == 0, rc
+    return out
+
+
+def row_l2_error(got: np.ndarray, want: np.ndarray) -> float:
+    """max over dst rows (ne0-runs) of max|got - want| / max(||want_row||_2, 1e-30)."""
+    g = got.reshape(-1, got.shape[-1]).astype(np.float64)
+    w = want.reshape(-1, want.shape[-1]).astype(np.float64)
+    norms = np.maximum(np.sqrt((w * w).sum(axis=1)), 1e-30)
+    return float((np.abs(g - w).max(axis=1) / norms).max())

@@ -1,0 +1,212 @@
+"""H3 parity: trc_hip_mul_mat_f32 (FP32 MFMA) against the oracle.
+
+Reference semantics: compute_mul_mat (src/backends/cpu/trc_cpu_ops.cpp:182-216).
+Bar (written here, from the benchmark's tolerance): for every dst row r (one
+ne0-run), max_i |y_ri - yhat_ri| / ||yhat_r||_2 <= 1e-4, where yhat is the oracle.
+The reference's own goldens additionally hold at their atol 1e-4 / rtol 1e-3.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from conftest import GOLDEN, announce
+from gpu_util import Dev, empty, gpu_mul_mat
+from traincpp_amd import hip as H
+from traincpp_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def g(name):
+    return np.load(GOLDEN / f"{name}.npy", allow_pickle=False)
+
+
+def as4(a):
+    return a.reshape((1,) * (4 - a.ndim) + a.shape)
+
+
+def ramp(n):
+    """The conformance tests' input ramp (tests/test_backend_conformance.cpp:130-135)."""
+    i = np.arange(n)
+    return ((i % 17) - 8).astype(np.float32) * np.float32(0.25)
+
+
+def t01(x):
+    return np.swapaxes(x, 2, 3)
+
+
+def run_views(A, a_view_fn, B, b_view_fn):
+    """Uploads the base arrays, runs the GPU on the views, returns (gpu, oracle)."""
+    da, db = Dev(A), Dev(B)
+    av, bv = a_view_fn(da.base), b_view_fn(db.base)
+    got = gpu_mul_mat(da, av, db, bv)
+    want = O.mul_mat(av, bv, threads=8)
+    da.free()
+    db.free()
+    return got, want
+
+
+@pytest.mark.parametrize("case", ["mul_mat", "mul_mat_batch", "mul_mat_batch_bcast_div", "mul_mat_batch_tile"])
+def test_reference_goldens(hip, case):
+    announce(f"mul_mat golden {case}")
+    a, b, want = as4(g(f"{case}_in0")), as4(g(f"{case}_in1")), g(f"{case}_out")
+    got, orc = run_views(a, lambda x: x, b, lambda x: x)
+    assert np.all(np.abs(got - want) <= 1e-4 + 1e-3 * np.abs(want))
+    assert O.row_l2_error(got, orc) <= TOL
+
+
+# The conformance suite's mul_mat cases (tests/test_backend_conformance.cpp:455-553,928-934):
+# (a base shape in ggml order, transpose a?, b base shape, transpose b?)
+CONFORMANCE = {
+    "basic": ((5, 3, 1, 1), False, (5, 4, 1, 1), False),
+    "transposed_a": ((3, 5, 1, 1), True, (5, 4, 1, 1), False),
+    "transposed_b": ((5, 3, 1, 1), False, (4, 5, 1, 1), True),
+    "tile_boundary": ((33, 70, 1, 1), False, (33, 66, 1, 1), False),
+    "batch": ((5, 3, 1, 1), False, (5, 4, 2, 3), False),
+    "batch_bcast_div": ((5, 3, 2, 1), False, (5, 4, 4, 1), False),
+    "batch_transposed": ((3, 5, 2, 2), True, (4, 5, 2, 2), True),
+    "batch_tile_boundary": ((33, 70, 1, 1), False, (33, 66, 2, 2), False),
+    "grid_batch_z": ((8, 4, 1, 1), False, (8, 4, 65, 1), False),
+}
+
+
+@pytest.mark.parametrize("name", list(CONFORMANCE))
+def test_conformance_cases(hip, name):
+    ane, ta, bne, tb = CONFORMANCE[name]
+    announce(f"mul_mat conformance {name}")
+    A = ramp(int(np.prod(ane))).reshape(ane[::-1])
+    B = ramp(int(np.prod(bne))).reshape(bne[::-1])
+    got, want = run_views(A, t01 if ta else (lambda x: x), B, t01 if tb else (lambda x: x))
+    # the conformance tolerance (test_backend_conformance.cpp:107) and the benchmark bar
+    assert np.all(np.abs(got - want) <= 1e-5 + 2e-4 * np.abs(want))
+    assert O.row_l2_error(got, want) <= TOL
+
+
+@pytest.mark.parametrize("case", ["grad_mul_mat_batch", "grad_mul_mat_batch_div"])
+def test_backward_goldens(hip, case):
+    """dA = transpose(mul_mat(transpose(dY), transpose(B))) (+ plane sum) and
+    dB = mul_mat(transpose(A), dY) (src/core/trc_autograd.cpp:487-503) on the GPU."""
+    announce(f"mul_mat backward golden {case}")
+    A, B = as4(g(f"{case}_in0")), as4(g(f"{case}_in1"))
+    Y, _ = run_views(A, lambda x: x, B, lambda x: x)
+    dY = (2.0 * Y).astype(np.float32)
+    dA_t, _ = run_views(dY, t01, B, t01)
+    dA_full = t01(dA_t)
+    a3, a2, b3, b2 = A.shape[0], A.shape[1], B.shape[0], B.shape[1]
+    dA = dA_full.reshape(b3 // a3, a3, b2 // a2, a2, *dA_full.shape[2:]).sum(axis=(0, 2))
+    dB, _ = run_views(A, t01, dY, lambda x: x)
+    for got, name in ((dA, "grad0"), (dB, "grad1")):
+        want = g(f"{case}_{name}")
+        assert np.all(np.abs(got - want) <= 1e-4 + 1e-3 * np.abs(want)), name
+
+
+@pytest.mark.parametrize("shape", [
+    # K, M, N, b2, b3, a2, a3
+    (1, 1, 1, 1, 1, 1, 1), (2, 33, 31, 1, 1, 1, 1), (17, 65, 129, 1, 1, 1, 1), (100, 130, 70, 3, 2, 3, 1),
+    (256, 256, 256, 1, 1, 1, 1), (513, 200, 300, 2, 1, 1, 1), (64, 128, 128, 4, 2, 2, 2), (7, 9, 11, 6, 1, 3, 1),
+])
+@pytest.mark.parametrize("layout", ["kk", "tk", "kt", "tt", "gen"])
+def test_random_shapes_and_layouts(hip, shape, layout):
+    K, M, N, b2, b3, a2, a3 = shape
+    rng = np.random.default_rng(K * 7 + M * 3 + N)
+    announce(f"mul_mat random {shape} {layout}")
+    if layout == "gen":
+        # every-other-element views: nb0 = 8 forces the scalar (generic) loaders
+        A = rng.standard_normal((a3, a2, M, 2 * K)).astype(np.float32)
+        B = rng.standard_normal((b3 * a3, b2 * a2, N, 2 * K)).astype(np.float32)
+        got, want = run_views(A, lambda x: x[..., ::2], B, lambda x: x[..., ::2])
+    else:
+        ta, tb = layout[0] == "t", layout[1] == "t"
+        A = rng.standard_normal((a3, a2, K, M) if ta else (a3, a2, M, K)).astype(np.float32)
+        B = rng.standard_normal((b3 * a3, b2 * a2, K, N) if tb else (b3 * a3, b2 * a2, N, K)).astype(np.float32)
+        got, want = run_views(A, t01 if ta else (lambda x: x), B, t01 if tb else (lambda x: x))
+    assert O.row_l2_error(got, want) <= TOL
+
+
+def sampled_oracle_cols(av, bv, cols):
+    """Oracle values of dst columns `cols` (dst rows in the row-L2 metric)."""
+    pa, ane, anb = O.base_ptr_and_meta(av)
+    pb, bne, bnb = O.base_ptr_and_meta(bv)
+    dne = [ane[1], bne[1], bne[2], bne[3]]
+    out = np.zeros((dne[3], dne[2], dne[1], dne[0]), dtype=np.float32)
+    _, _, dnb = O.base_ptr_and_meta(out)
+    for j in cols:
+        rc = O.oracle().orc_mul_mat_cols(pa, O.NE(*ane), O.NB(*anb), pb, O.NE(*bne), O.NB(*bnb), out.ctypes.data,
+                                         O.NE(*dne), O.NB(*dnb), int(j), int(j) + 1, 8)
+        assert rc == 0
+    return out[:, :, cols, :]
+
+
+def config3_inputs():
+    t = 7  # Q5_1 weights, dequantized on the GPU exactly as the oracle does
+    n = 4096 * 4096 // 32
+    raw = synth.block_bytes(synth.quant_blocks(t, n, synth.config_seed(3, 0)))
+    W = O.dequant(t, raw, threads=8).reshape(1, 1, 4096, 4096)
+    X = synth.normal(synth.config_seed(3, 1), 4096 * 512).reshape(1, 1, 512, 4096)
+    dY = synth.normal(synth.config_seed(3, 2), 4096 * 512, 0.0, 1e-2).reshape(1, 1, 512, 4096)
+    return W, X, dY
+
+
+COLS = [0, 1, 63, 64, 200, 511]
+
+
+@pytest.fixture(scope="module")
+def cfg3():
+    return config3_inputs()
+
+
+@pytest.mark.parametrize("product", ["Y=W.X", "dX=W^T.dY", "dW^T=dY^T.X^T"])
+def test_config3_full_size(hip, cfg3, product):
+    """The linear layer's three products at 4096 x 4096 x 512, checked on sampled
+    dst rows against the oracle."""
+    W, X, dY = cfg3
+    announce(f"mul_mat cfg3 {product}")
+    if product == "Y=W.X":
+        A, af, B, bf, cols = W, (lambda x: x), X, (lambda x: x), COLS
+    elif product == "dX=W^T.dY":
+        A, af, B, bf, cols = W, t01, dY, (lambda x: x), COLS
+    else:
+        A, af, B, bf, cols = dY, t01, X, t01, [0, 1, 4095, 1000, 2048]
+    da, db = Dev(A), Dev(B)
+    av, bv = af(da.base), bf(db.base)
+    got = gpu_mul_mat(da, av, db, bv)
+    want = sampled_oracle_cols(av, bv, cols)
+    assert O.row_l2_error(got[:, :, cols, :], want) <= TOL
+    assert np.isfinite(got).all()
+    da.free()
+    db.free()
+
+
+def test_config4_broadcast_permuted(hip):
+    """src0 ne=[128,1024,8,4] x src1 = permute(base[128,32,512,4], 0,2,1,3)
+    (ne=[128,512,32,4], nb1 > nb2), planes broadcast (i2%8, i3%4)."""
+    announce("mul_mat cfg4")
+    A = synth.normal(synth.config_seed(4, 0), 128 * 1024 * 8 * 4).reshape(4, 8, 1024, 128)
+    base = synth.normal(synth.config_seed(4, 1), 128 * 32 * 512 * 4).reshape(4, 512, 32, 128)
+    da, db = Dev(A), Dev(base)
+    bv = np.swapaxes(db.base, 1, 2)  # ggml permute(0,2,1,3)
+    ne, nb = O.view_meta(bv)
+    assert ne == [128, 512, 32, 4] and nb == [4, 16384, 512, 8388608]
+    got = gpu_mul_mat(da, da.base, db, bv)
+    cols = [0, 7, 300, 511]
+    want = sampled_oracle_cols(da.base, bv, cols)
+    assert O.row_l2_error(got[:, :, cols, :], want) <= TOL
+    da.free()
+    db.free()
+
+
+def test_shape_errors_are_rejected(hip):
+    a = empty((1, 1, 4, 8))
+    b = empty((1, 1, 4, 6))
+    d = empty((1, 1, 4, 4))
+    with pytest.raises(H.HipError) as e:
+        H.mul_mat_f32(a.tensor(), b.tensor(), d.tensor())  # K 8 vs 6
+    assert e.value.code == H.E_SHAPE
+    b2 = empty((1, 3, 4, 8))
+    a2 = empty((1, 2, 4, 8))
+    d2 = empty((1, 3, 4, 4))
+    with pytest.raises(H.HipError) as e:
+        H.mul_mat_f32(a2.tensor(), b2.tensor(), d2.tensor())  # 3 % 2 != 0
+    assert e.value.code == H.E_SHAPE

@@ -1,0 +1,148 @@
+"""Pins the oracle's mul_mat (oracle/oracle.cpp, restating
+src/backends/cpu/trc_cpu_ops.cpp:182-216) on the CPU.
+
+  * the reference's KATs (tests/test_ops.cpp:185-275);
+  * the reference's PyTorch goldens tests/golden/mul_mat*.npy, at the reference's
+    tolerance (atol 1e-4 + rtol 1e-3, tests/test_golden.cpp:190-201);
+  * the backward goldens grad_mul_mat*.npy through the compositions autograd
+    emits (src/core/trc_autograd.cpp:487-503), tests/test_grad_golden.cpp:261;
+  * a float64 brute force with the recursive-summation error bound
+    |err| <= gamma_K * sum|a||b|, on random shapes incl. broadcast planes;
+  * the reference library's own mul_mat on permuted views (oracle/_ref),
+    bit for bit (same k order, same roundings).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from conftest import GOLDEN
+
+
+def g(name):
+    return np.load(GOLDEN / f"{name}.npy", allow_pickle=False)
+
+
+def as4(a):
+    return a.reshape((1,) * (4 - a.ndim) + a.shape)
+
+
+# ---------------------------------------------------------------- KATs (test_ops.cpp:185-275)
+
+def test_kat_2x2_times_2x3():
+    a = np.float32([1, 2, 3, 4]).reshape(1, 1, 2, 2)        # ggml [k=2, m=2]
+    b = np.float32([1, 2, 3, 4, 5, 6]).reshape(1, 1, 3, 2)  # ggml [k=2, n=3]
+    out = O.mul_mat(a, b)
+    assert out.shape == (1, 1, 3, 2)
+    assert np.array_equal(out.reshape(-1), np.float32([5, 11, 11, 25, 17, 39]))
+
+
+def test_kat_batch_broadcast():
+    a = np.float32([1, 2, 3, 4]).reshape(1, 1, 2, 2)
+    b = np.arange(1, 9, dtype=np.float32).reshape(1, 2, 2, 2)  # [k=2, n=2, b2=2]
+    out = O.mul_mat(a, b)
+    assert np.array_equal(out.reshape(-1), np.float32([5, 11, 11, 25, 17, 39, 23, 53]))
+
+
+def test_kat_modulo_broadcast():
+    a = np.float32([1, 2]).reshape(1, 2, 1, 1)           # [k=1, m=1, a2=2]
+    b = np.float32([1, 2, 3, 4]).reshape(2, 2, 1, 1)     # [k=1, n=1, b2=2, b3=2]
+    out = O.mul_mat(a, b)
+    assert np.array_equal(out.reshape(-1), np.float32([1, 4, 3, 8]))
+
+
+# ---------------------------------------------------------------- PyTorch goldens
+
+@pytest.mark.parametrize("case", ["mul_mat", "mul_mat_batch", "mul_mat_batch_bcast_div", "mul_mat_batch_tile"])
+def test_forward_goldens(case):
+    a, b, want = g(f"{case}_in0"), g(f"{case}_in1"), g(f"{case}_out")
+    got = O.mul_mat(as4(a), as4(b))
+    assert got.shape == want.shape
+    assert np.all(np.abs(got - want) <= 1e-4 + 1e-3 * np.abs(want))
+
+
+def transpose01(x):
+    """ggml transpose (permute 1,0,2,3) of a 4-D numpy view: swaps the two
+    innermost numpy axes without copying."""
+    return np.swapaxes(x, 2, 3)
+
+
+@pytest.mark.parametrize("case", ["grad_mul_mat_batch", "grad_mul_mat_batch_div"])
+def test_backward_goldens(case):
+    A, B = as4(g(f"{case}_in0")), as4(g(f"{case}_in1"))
+    Y = O.mul_mat(A, B)
+    loss = np.float64((Y.astype(np.float64) ** 2).sum())
+    assert abs(loss - g(f"{case}_loss").reshape(-1)[0]) <= 1e-4 + 1e-3 * abs(loss)
+    dY = (2.0 * Y).astype(np.float32)  # d(sum(y^2))/dy
+    # dA = transpose(mul_mat(transpose(dY), transpose(B))), summed over the planes
+    # that A was broadcast to (repeat_back), trc_autograd.cpp:492-496
+    dA_full = transpose01(O.mul_mat(transpose01(dY), transpose01(B)))
+    a3, a2 = A.shape[0], A.shape[1]
+    b3, b2 = B.shape[0], B.shape[1]
+    dA = dA_full.reshape(b3 // a3, a3, b2 // a2, a2, *dA_full.shape[2:]).sum(axis=(0, 2))
+    # dB = mul_mat(transpose(A), dY), trc_autograd.cpp:500
+    dB = O.mul_mat(transpose01(A), dY)
+    for got, name in ((dA, "grad0"), (dB, "grad1")):
+        want = g(f"{case}_{name}")
+        assert got.shape == want.shape
+        assert np.all(np.abs(got - want) <= 1e-4 + 1e-3 * np.abs(want)), name
+
+
+# ---------------------------------------------------------------- brute force with an error bound
+
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1, 1, 1), (7, 5, 3, 1, 1, 1), (33, 70, 66, 2, 2, 1),
+                                   (64, 17, 9, 3, 4, 3), (300, 8, 40, 1, 2, 1)])
+def test_brute_force_bound(shape):
+    K, M, N, b2, b3, a2 = shape
+    rng = np.random.default_rng(sum(shape))
+    a = rng.standard_normal((1, a2, M, K)).astype(np.float32)
+    b = rng.standard_normal((b3, b2 * a2, N, K)).astype(np.float32)
+    got = O.mul_mat(a, b).astype(np.float64)
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    i2 = np.arange(b2 * a2) % a2
+    exact = np.einsum("pmk,qpnk->qpnm", a64[0][i2], b64)
+    bound = np.einsum("pmk,qpnk->qpnm", np.abs(a64[0][i2]), np.abs(b64))
+    u = 2.0**-24
+    gamma = K * u / (1 - K * u)
+    assert np.all(np.abs(got - exact) <= gamma * bound + 1e-30)
+
+
+def test_bad_shape_is_rejected():
+    a = np.zeros((1, 1, 3, 4), np.float32)
+    b = np.zeros((1, 1, 3, 5), np.float32)
+    pa, ane, anb = O.base_ptr_and_meta(a)
+    pb, bne, bnb = O.base_ptr_and_meta(b)
+    out = np.zeros(9, np.float32)
+    rc = O.oracle().orc_mul_mat(pa, O.NE(*ane), O.NB(*anb), pb, O.NE(*bne), O.NB(*bnb), out.ctypes.data,
+                                O.NE(3, 3, 1, 1), O.NB(4, 12, 36, 36), 1)
+    assert rc == -1
+
+
+# ---------------------------------------------------------------- vs the reference library
+
+REF_CASES = [
+    # (a base ne, a axes, b base ne, b axes)
+    ((5, 3, 1, 1), (0, 1, 2, 3), (5, 4, 1, 1), (0, 1, 2, 3)),        # basic
+    ((3, 5, 1, 1), (1, 0, 2, 3), (5, 4, 1, 1), (0, 1, 2, 3)),        # transposed a
+    ((5, 3, 1, 1), (0, 1, 2, 3), (4, 5, 1, 1), (1, 0, 2, 3)),        # transposed b
+    ((33, 70, 1, 1), (0, 1, 2, 3), (33, 66, 2, 2), (0, 1, 2, 3)),    # tile boundary + batch
+    ((5, 3, 2, 1), (0, 1, 2, 3), (5, 4, 4, 1), (0, 1, 2, 3)),        # modulo broadcast
+    ((3, 5, 2, 2), (1, 0, 2, 3), (4, 5, 2, 2), (1, 0, 2, 3)),        # batch + both transposed
+    ((16, 24, 2, 2), (0, 1, 2, 3), (16, 6, 10, 4), (0, 2, 1, 3)),    # cfg-4 style permuted src1
+    ((24, 40, 1, 1), (1, 0, 2, 3), (48, 40, 1, 1), (1, 0, 2, 3)),    # dW-style: both K-strided
+]
+
+
+@pytest.mark.skipif(not O.have_ref(), reason="oracle/_ref not built (reference checkout absent)")
+@pytest.mark.parametrize("case", REF_CASES, ids=[str(i) for i in range(len(REF_CASES))])
+def test_bitwise_vs_reference_library(case):
+    ane, pa, bne, pb = case
+    rng = np.random.default_rng(len(str(case)))
+    A = rng.standard_normal(ane[::-1]).astype(np.float32)
+    B = rng.standard_normal(bne[::-1]).astype(np.float32)
+    want = O.ref_mul_mat(A, pa, B, pb)
+    # the same views in numpy: ggml permute(axes) -> numpy transpose of reversed axes
+    def view(x, axes):
+        np_axes = [3 - axes[3 - i] for i in range(4)]
+        return np.transpose(x, np_axes)
+    got = O.mul_mat(view(A, pa), view(B, pb), threads=3)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -1,0 +1,51 @@
+// Shared definitions for the gfx950 kernels of libtrc_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "trc_hip_abi.h"
+
+namespace trc_hip {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+// GGUF legacy block sizes in bytes (include/traincpp/trc_types.h values,
+// src/core/trc_types.cpp:27-31). Every block holds 32 elements.
+constexpr int QK = 32;
+
+__host__ __device__ constexpr int block_bytes(int type) {
+    return type == TRC_HIP_TYPE_Q4_0   ? 18
+           : type == TRC_HIP_TYPE_Q4_1 ? 20
+           : type == TRC_HIP_TYPE_Q5_0 ? 22
+           : type == TRC_HIP_TYPE_Q5_1 ? 24
+           : type == TRC_HIP_TYPE_Q8_0 ? 34
+                                       : 0;
+}
+
+// IEEE binary16 -> binary32 (v_cvt_f32_f16). Exact on every finite input,
+// subnormals included, as is the reference's bit-trick decode
+// (src/core/trc_float.h:23-40).
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    return (float) __builtin_bit_cast(_Float16, (uint16_t) h);
+}
+
+// Launch-side error reporting, implemented in abi.hip.
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// Kernel launchers (one per kernel family). They validate what the kernels
+// assume, enqueue on `stream` and return a trc_hip_status / hipError_t.
+int launch_dequant(int type, const void* blocks, int64_t n_blocks, float* dst, hipStream_t stream);
+int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d,
+                       hipStream_t stream);
+int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x,
+                   int64_t N, size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream);
+int launch_fill_f32(float* dst, float value, int64_t count, hipStream_t stream);
+int launch_cpy(const trc_hip_tensor& src, const trc_hip_tensor& dst, size_t elem_size,
+               hipStream_t stream);
+
+}  // namespace trc_hip
