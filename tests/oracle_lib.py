@@ -106,13 +106,13 @@ def ref_dequant(type_: int, blocks: np.ndarray, tmp_dir: str) -> np.ndarray:
 def view_meta(arr: np.ndarray):
     """(ne, nb) in ggml order for a numpy array viewed as a ggml tensor (numpy
     axes reversed: numpy shape (ne3, ne2, ne1, ne0))."""
-    assert arr.dtype == np.float32 and arr.ndim <= 4
+    assert arr.ndim <= 4
     shape = list(arr.shape)[::-1] + [1] * (4 - arr.ndim)
     strides = list(arr.strides)[::-1]
     nb = strides + [0] * (4 - arr.ndim)
     # fill strides of the padded unit dims with the extent of the last real one
     for i in range(arr.ndim, 4):
-        nb[i] = (nb[i - 1] * shape[i - 1]) if i > 0 else 4
+        nb[i] = (nb[i - 1] * shape[i - 1]) if i > 0 else arr.itemsize
     return shape, nb
 
 

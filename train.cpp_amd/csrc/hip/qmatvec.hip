@@ -169,6 +169,556 @@ __global__ __launch_bounds__(QV_THREADS) void k_qmatvec(const uint8_t* __restric
     }
 }
 
+// ---------------------------------------------------------------- N = 1 (decode) kernel
+//
+// The batch-1 product is a pure stream over W, so this kernel is organised
+// around moving W at full HBM rate:
+//   - W is staged through LDS with fully coalesced dwordx4 loads: a wave copies
+//     ROWS row-chunks of CH blocks (CH*BYTES bytes each, a multiple of 16) with
+//     every lane issuing all of its loads before its LDS writes.
+//   - Each lane then decodes one pair of adjacent blocks per row from LDS.
+//     A pair starts on a 4-byte boundary for every format (2*BYTES is a
+//     multiple of 4), so the decode uses aligned dword reads and byte-align
+//     shifts, never unaligned accesses.
+//   - A lane always owns the same pair column, so its 64 x values and their
+//     per-block sums stay in registers for every row the wave processes; with
+//     K = 32*CH (4096) they are loaded once per wave for the whole launch.
+//   - The integer quants are converted with v_cvt_f32_ubyte (1 op per element);
+//     the bias (8, 16, or 128 for Q8_0 after flipping the sign bits) is removed
+//     once per block through the block's x sum.
+// Waves are persistent over tiles of ROWS rows and only synchronise with
+// themselves (each wave owns its LDS region).
+
+constexpr int QV1_WAVES = 4;
+constexpr int QV1_CH = 128;  // blocks per staged row chunk
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint32_t align2(uint32_t hi, uint32_t lo) {
+    return __builtin_amdgcn_alignbyte(hi, lo, 2);  // bytes 2..5 of {hi:lo}
+}
+
+__device__ __forceinline__ uint32_t spread4(uint32_t four) {  // bits 0..3 -> bit 4 of bytes 0..3
+    return ((four & 1u) << 4) | ((four & 2u) << 11) | ((four & 4u) << 18) | ((four & 8u) << 25);
+}
+
+// sum_{c<4} byte_c(q) * x[c]
+__device__ __forceinline__ float dot4_ub(uint32_t q, f4 x, float acc) {
+    acc += (float) (q & 0xFFu) * x.x;
+    acc += (float) ((q >> 8) & 0xFFu) * x.y;
+    acc += (float) ((q >> 16) & 0xFFu) * x.z;
+    acc += (float) (q >> 24) * x.w;
+    return acc;
+}
+
+// One decoded block in registers: scale bits, min bits, 5th-bit mask, quant words.
+struct Blk {
+    uint32_t d, m, qh;
+    uint32_t q[8];
+};
+
+// Extracts the two blocks of a pair from its aligned dwords (pw = pair start).
+template <int TYPE>
+__device__ __forceinline__ void read_pair(const uint32_t* pw, Blk& A, Blk& B) {
+    if constexpr (TYPE == TRC_HIP_TYPE_Q4_0) {  // 36 B: A at 0, B at 18
+        uint32_t w[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) w[i] = pw[i];
+        A.d = w[0] & 0xFFFFu;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) A.q[i] = align2(w[i + 1], w[i]);
+        B.d = w[4] >> 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) B.q[i] = w[5 + i];
+    } else if constexpr (TYPE == TRC_HIP_TYPE_Q4_1) {  // 40 B: A at 0, B at 20
+        uint32_t w[10];
+#pragma unroll
+        for (int i = 0; i < 10; ++i) w[i] = pw[i];
+        A.d = w[0] & 0xFFFFu;
+        A.m = w[0] >> 16;
+        B.d = w[5] & 0xFFFFu;
+        B.m = w[5] >> 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            A.q[i] = w[1 + i];
+            B.q[i] = w[6 + i];
+        }
+    } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_0) {  // 44 B: A at 0, B at 22
+        uint32_t w[11];
+#pragma unroll
+        for (int i = 0; i < 11; ++i) w[i] = pw[i];
+        A.d = w[0] & 0xFFFFu;
+        A.qh = align2(w[1], w[0]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) A.q[i] = align2(w[i + 2], w[i + 1]);
+        B.d = w[5] >> 16;
+        B.qh = w[6];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) B.q[i] = w[7 + i];
+    } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_1) {  // 48 B: A at 0, B at 24
+        uint32_t w[12];
+#pragma unroll
+        for (int i = 0; i < 12; ++i) w[i] = pw[i];
+        A.d = w[0] & 0xFFFFu;
+        A.m = w[0] >> 16;
+        A.qh = w[1];
+        B.d = w[6] & 0xFFFFu;
+        B.m = w[6] >> 16;
+        B.qh = w[7];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            A.q[i] = w[2 + i];
+            B.q[i] = w[8 + i];
+        }
+    } else {  // Q8_0, 68 B: A at 0, B at 34
+        uint32_t w[17];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) w[i] = pw[i];
+        A.d = w[0] & 0xFFFFu;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) A.q[i] = align2(w[i + 1], w[i]);
+        B.d = w[8] >> 16;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) B.q[i] = w[9 + i];
+    }
+}
+
+// d * sum_e q_e x_e (+ m * sum_e x_e) for one block; xv holds the block's 32 x
+// values as 8 float4 (elements 4c..4c+3), xs their sum.
+template <int TYPE>
+__device__ __forceinline__ float block_dot(const Blk& b, const f4* xv, float xs) {
+    float s = 0.f;
+    if constexpr (TYPE == TRC_HIP_TYPE_Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = dot4_ub(b.q[i] ^ 0x80808080u, xv[i], s);  // q + 128 as unsigned
+        return half_bits_to_float(b.d) * (s - 128.f * xs);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t lo = b.q[i] & 0x0F0F0F0Fu;
+            uint32_t hi = (b.q[i] >> 4) & 0x0F0F0F0Fu;
+            if constexpr (TYPE == TRC_HIP_TYPE_Q5_0 || TYPE == TRC_HIP_TYPE_Q5_1) {
+                lo |= spread4((b.qh >> (4 * i)) & 0xFu);
+                hi |= spread4((b.qh >> (16 + 4 * i)) & 0xFu);
+            }
+            s = dot4_ub(lo, xv[i], s);
+            s = dot4_ub(hi, xv[4 + i], s);
+        }
+        const float d = half_bits_to_float(b.d);
+        if constexpr (TYPE == TRC_HIP_TYPE_Q4_0) return d * (s - 8.f * xs);
+        if constexpr (TYPE == TRC_HIP_TYPE_Q5_0) return d * (s - 16.f * xs);
+        return d * s + half_bits_to_float(b.m) * xs;  // Q4_1, Q5_1
+    }
+}
+
+template <int TYPE, int ROWS, int HALF>
+__global__ __launch_bounds__(QV1_WAVES * 64) void k_qmatvec_n1(const uint8_t* __restrict__ W, int64_t nblk,
+                                                              int64_t M, int64_t nb1_w,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y) {
+    constexpr int BYTES = block_bytes(TYPE);
+    constexpr int CHB = QV1_CH * BYTES;  // staged bytes per row chunk
+    constexpr int F4R = CHB / 16;        // float4s per row chunk
+    constexpr int NPH = HALF * F4R / 64; // float4s per lane for HALF rows
+    constexpr int PARTS = ROWS / HALF;
+    static_assert(CHB % 16 == 0 && (HALF * F4R) % 64 == 0 && ROWS % HALF == 0, "staging must split evenly");
+    __shared__ __attribute__((aligned(16))) uint8_t stage[QV1_WAVES * HALF * CHB];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    uint8_t* my = stage + wave * HALF * CHB;
+    const int64_t nchunks = (nblk + QV1_CH - 1) / QV1_CH;
+    const int64_t ntiles = (M + ROWS - 1) / ROWS;
+    const int64_t nwaves = (int64_t) gridDim.x * QV1_WAVES;
+
+    f4 xv[16];
+    float xs[2];
+    auto load_x = [&](int64_t c) {
+        const int64_t b0 = c * QV1_CH + 2 * lane;  // first block of this lane's pair
+        if (b0 < nblk) {
+            const f4* xp = (const f4*) (x + b0 * QK);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xv[i] = xp[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xv[i] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s += (xv[8 * h + i].x + xv[8 * h + i].y) + (xv[8 * h + i].z + xv[8 * h + i].w);
+            xs[h] = s;
+        }
+    };
+
+    // rows [r0, r0 + HALF) of the current tile are in LDS: accumulate them
+    auto compute_half = [&](float* acc, int64_t row0, int r0, int64_t cb) {
+        if (2 * lane < cb) {
+#pragma unroll
+            for (int r = 0; r < HALF; ++r) {
+                if (row0 + r0 + r < M) {
+                    Blk A, B;
+                    read_pair<TYPE>((const uint32_t*) (my + r * CHB + lane * 2 * BYTES), A, B);
+                    acc[r0 + r] += block_dot<TYPE>(A, xv, xs[0]) + block_dot<TYPE>(B, xv + 8, xs[1]);
+                }
+            }
+        }
+    };
+
+    for (int64_t tile = (int64_t) blockIdx.x * QV1_WAVES + wave; tile < ntiles; tile += nwaves) {
+        const int64_t row0 = tile * ROWS;
+        float acc[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) acc[r] = 0.f;
+
+        for (int64_t c = 0; c < nchunks; ++c) {
+            const int64_t cb = nblk - c * QV1_CH < QV1_CH ? nblk - c * QV1_CH : QV1_CH;
+            const uint8_t* src = W + row0 * nb1_w + c * CHB;
+            if (cb == QV1_CH && row0 + ROWS <= M) {
+                // whole tile: issue every load of the tile (and x) before using any
+                f4 t[PARTS * NPH];
+#pragma unroll
+                for (int k = 0; k < PARTS * NPH; ++k) {
+                    const int i = lane + 64 * k;
+                    t[k] = *(const f4*) (src + (i / F4R) * nb1_w + (i % F4R) * 16);
+                }
+                if (c == 0 || nchunks > 1) {
+                    if (tile == (int64_t) blockIdx.x * QV1_WAVES + wave || nchunks > 1) load_x(c);
+                }
+#pragma unroll
+                for (int p = 0; p < PARTS; ++p) {
+                    wave_lds_sync();  // every lane is done reading the previous part
+#pragma unroll
+                    for (int k = 0; k < NPH; ++k) ((f4*) my)[lane + 64 * k] = t[p * NPH + k];
+                    wave_lds_sync();  // the staged part is visible to every lane
+                    compute_half(acc, row0, p * HALF, cb);
+                }
+            } else {
+                if (tile == (int64_t) blockIdx.x * QV1_WAVES + wave || nchunks > 1) load_x(c);
+                const int nf4 = (int) (cb * BYTES / 16);
+                for (int p = 0; p < PARTS; ++p) {
+                    wave_lds_sync();
+                    for (int r = 0; r < HALF; ++r) {
+                        if (row0 + p * HALF + r >= M) break;
+                        for (int f = lane; f < nf4; f += 64) {
+                            ((f4*) (my + r * CHB))[f] = *(const f4*) (src + (p * HALF + r) * nb1_w + f * 16);
+                        }
+                    }
+                    wave_lds_sync();
+                    compute_half(acc, row0, p * HALF, cb);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            float v = acc[r];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+            acc[r] = v;
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                if (row0 + r < M) y[row0 + r] = acc[r];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- N = 1, integer-dot kernel
+//
+// The FP32 formulation costs about 2.4 VALU operations per weight element
+// (convert the nibble, multiply-add, unpack), which makes a batch-1 matvec
+// VALU-bound on gfx950 well before it is HBM-bound. This kernel moves the
+// multiply-adds onto the packed integer dot instructions instead:
+//
+//   - Each workgroup converts its chunk of x (4096 elements) once to block
+//     fixed point: per 32-element block b, X_e = rint(x_e * 2^s_b) with s_b
+//     chosen so |X_e| < 2^22, i.e. a 24-bit two's-complement integer with 22
+//     significant bits for the block maximum. The three bytes of every X_e are
+//     transposed into byte planes P0 (bits 0-7), P1 (8-15), P2 (16-23, signed)
+//     so that one dword of a plane holds 4 consecutive elements, the same
+//     element order as the quant bytes after the nibble split. Planes, 2^-s_b
+//     and the block sums of x go to LDS, then into each lane's registers.
+//   - Per row block, each quant word (8 elements) is split into low/high nibble
+//     bytes (3 ops) and multiplied against the planes with v_dot4_u32_u8 (P0,
+//     P1) and v_dot4_i32_i8 (P2): exact integer products and sums. The three
+//     plane sums are combined in float, scaled by 2^-s_b and by d; the bias
+//     (8 or 16) and the min (Q4_1/Q5_1) go through the block sum of x.
+//   - About 1.1 VALU ops per element instead of 2.4. The only rounding beyond
+//     FP32's is the 24-bit representation of x, whose error per element is at
+//     most 2^-23 of the block's largest |x|; the reference's own sequential
+//     FP32 sum of 32 products carries an error bound of the same order.
+//   - Each lane owns one pair of blocks of the chunk for every row its wave
+//     processes (pairs start on 4-byte boundaries for all formats); a wave
+//     handles a contiguous run of at most QD_RMAX rows with QD_PREFETCH rows of
+//     loads in flight; the per-row sums are reduced across the wave at the end.
+
+constexpr int QD_CH = 128;        // blocks per chunk of K (one lane = one pair)
+constexpr int QD_RMAX = 8;        // rows per wave at most
+constexpr int QD_PREFETCH = 3;    // rows whose loads are in flight
+constexpr int QD_PSTRIDE = 52;    // LDS dwords per pair of planes (48 + 4: conflict-free b128 reads)
+
+template <int TYPE>
+struct QdFmt {
+    static constexpr int BYTES = block_bytes(TYPE);
+    static constexpr int PAIR_WORDS = 2 * BYTES / 4;  // 9, 10, 11, 12
+};
+
+// x chunk -> byte planes in LDS. Thread t converts elements [16t, 16t+16) of
+// the chunk: half h = t&1 of block b = t>>1 (partner lane t^1 holds the other half).
+__device__ __forceinline__ void qd_load_x(const float* __restrict__ xc, int64_t cb, f4* v) {
+    const int t = threadIdx.x;
+    const bool active = (t >> 1) < cb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = active ? ((const f4*) xc)[4 * t + i] : f4{0.f, 0.f, 0.f, 0.f};
+}
+
+__device__ __forceinline__ void qd_prologue(const f4* v, int64_t cb, uint32_t* planes, float* scale, float* xsum) {
+    const int t = threadIdx.x;
+    const int b = t >> 1, h = t & 1;
+    const bool active = b < cb;
+    float mx = 0.f, sm = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        sm += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    sm += __shfl_xor(sm, 1, 64);
+    // s = 22 - E with mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^22
+    const int s = mx > 0.f ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
+    const bool finite = __builtin_isfinite(mx);
+    uint32_t P[3][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].x, s));
+        const uint32_t bb = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].y, s));
+        const uint32_t c = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].z, s));
+        const uint32_t d = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].w, s));
+        const uint32_t t_ab = __builtin_amdgcn_perm(bb, a, 0x05010400u);  // a0 b0 a1 b1
+        const uint32_t t_cd = __builtin_amdgcn_perm(d, c, 0x05010400u);   // c0 d0 c1 d1
+        P[0][i] = __builtin_amdgcn_perm(t_cd, t_ab, 0x05040100u);         // a0 b0 c0 d0
+        P[1][i] = __builtin_amdgcn_perm(t_cd, t_ab, 0x07060302u);         // a1 b1 c1 d1
+        P[2][i] = __builtin_amdgcn_perm(bb, a, 0x0c0c0602u) | __builtin_amdgcn_perm(d, c, 0x06020c0cu);  // a2 b2 c2 d2
+    }
+    if (active) {
+        // pair l = b>>1; within the pair, block (b&1) owns groups 8*(b&1) .. +7:
+        // groups 0-3 are elements 0-15 (half 0), groups 4-7 elements 16-31 (half 1)
+        uint32_t* dst = planes + (b >> 1) * QD_PSTRIDE + 8 * (b & 1) + 4 * h;
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+            *(uint4*) (dst + 16 * p) = uint4{P[p][0], P[p][1], P[p][2], P[p][3]};
+        }
+        if (h == 0) {
+            scale[b] = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
+            xsum[b] = sm;
+        }
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void qd_unpack(uint32_t w, uint32_t qh_bits8, uint32_t& lo, uint32_t& hi) {
+    lo = w & 0x0F0F0F0Fu;
+    hi = (w >> 4) & 0x0F0F0F0Fu;
+    if constexpr (TYPE == TRC_HIP_TYPE_Q5_0 || TYPE == TRC_HIP_TYPE_Q5_1) {
+        // qh_bits8: bits 0-3 = 5th bits of the 4 low elements, bits 4-7 of the 4 high ones
+        lo |= ((qh_bits8 & 0xFu) * 0x00204081u & 0x01010101u) << 4;
+        hi |= (((qh_bits8 >> 4) & 0xFu) * 0x00204081u & 0x01010101u) << 4;
+    }
+}
+
+// One block of one row: 4 quant words against this lane's 8 plane groups.
+template <int TYPE>
+__device__ __forceinline__ float qd_block(const uint32_t* q, uint32_t qh, uint32_t d_bits, uint32_t m_bits,
+                                          const uint32_t (*P)[8], float scale, float xs) {
+    // six independent accumulation chains (plane x low/high nibble)
+    uint32_t s0 = 0, s1 = 0, t0 = 0, t1 = 0;
+    int s2 = 0, t2 = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t lo, hi;
+        const uint32_t bits = ((qh >> (4 * w)) & 0xFu) | (((qh >> (16 + 4 * w)) & 0xFu) << 4);
+        qd_unpack<TYPE>(q[w], bits, lo, hi);
+        s0 = __builtin_amdgcn_udot4(lo, P[0][w], s0, false);
+        s1 = __builtin_amdgcn_udot4(lo, P[1][w], s1, false);
+        s2 = __builtin_amdgcn_sdot4((int) lo, (int) P[2][w], s2, false);
+        t0 = __builtin_amdgcn_udot4(hi, P[0][4 + w], t0, false);
+        t1 = __builtin_amdgcn_udot4(hi, P[1][4 + w], t1, false);
+        t2 = __builtin_amdgcn_sdot4((int) hi, (int) P[2][4 + w], t2, false);
+    }
+    s0 += t0;
+    s1 += t1;
+    s2 += t2;
+    // sum_e q_e X_e = s0 + 256 s1 + 65536 s2 (s0 + 256 s1 < 2^25)
+    const float qx = __builtin_fmaf((float) s2, 65536.f, (float) (s0 + (s1 << 8))) * scale;
+    const float d = half_bits_to_float(d_bits);
+    if constexpr (TYPE == TRC_HIP_TYPE_Q4_0) return d * __builtin_fmaf(-8.f, xs, qx);
+    if constexpr (TYPE == TRC_HIP_TYPE_Q5_0) return d * __builtin_fmaf(-16.f, xs, qx);
+    return __builtin_fmaf(d, qx, half_bits_to_float(m_bits) * xs);
+}
+
+// Decodes the dwords of a pair (pw, PAIR_WORDS of them) into the fields of its two blocks.
+template <int TYPE>
+__device__ __forceinline__ float qd_pair(const uint32_t* w, const uint32_t (*PA)[8], const uint32_t (*PB)[8],
+                                         const float* sc, const float* xs) {
+    uint32_t qa[4], qb[4];
+    if constexpr (TYPE == TRC_HIP_TYPE_Q4_0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { qa[i] = align2(w[i + 1], w[i]); qb[i] = w[5 + i]; }
+        return qd_block<TYPE>(qa, 0, w[0] & 0xFFFFu, 0, PA, sc[0], xs[0]) +
+               qd_block<TYPE>(qb, 0, w[4] >> 16, 0, PB, sc[1], xs[1]);
+    } else if constexpr (TYPE == TRC_HIP_TYPE_Q4_1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { qa[i] = w[1 + i]; qb[i] = w[6 + i]; }
+        return qd_block<TYPE>(qa, 0, w[0] & 0xFFFFu, w[0] >> 16, PA, sc[0], xs[0]) +
+               qd_block<TYPE>(qb, 0, w[5] & 0xFFFFu, w[5] >> 16, PB, sc[1], xs[1]);
+    } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { qa[i] = align2(w[i + 2], w[i + 1]); qb[i] = w[7 + i]; }
+        return qd_block<TYPE>(qa, align2(w[1], w[0]), w[0] & 0xFFFFu, 0, PA, sc[0], xs[0]) +
+               qd_block<TYPE>(qb, w[6], w[5] >> 16, 0, PB, sc[1], xs[1]);
+    } else {  // Q5_1
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { qa[i] = w[2 + i]; qb[i] = w[8 + i]; }
+        return qd_block<TYPE>(qa, w[1], w[0] & 0xFFFFu, w[0] >> 16, PA, sc[0], xs[0]) +
+               qd_block<TYPE>(qb, w[7], w[6] & 0xFFFFu, w[6] >> 16, PB, sc[1], xs[1]);
+    }
+}
+
+// Sum over the 64 lanes of a wave with DPP row operations (no LDS traffic);
+// the total lands in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK,
+                                                                  0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+    v += dpp_f32<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141, 0xF>(v);  // row_half_mirror: sums of 8
+    v += dpp_f32<0x140, 0xF>(v);  // row_mirror: sums of 16 in every row
+    v += dpp_f32<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_f32<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_qmatvec_dot(const uint8_t* __restrict__ W, int64_t nblk, int64_t M,
+                                                     int64_t nb1_w, const float* __restrict__ x,
+                                                     float* __restrict__ y, int rpw) {
+    constexpr int BYTES = block_bytes(TYPE);
+    constexpr int PW = QdFmt<TYPE>::PAIR_WORDS;
+    __shared__ __attribute__((aligned(16))) uint32_t planes[(QD_CH / 2) * QD_PSTRIDE];
+    __shared__ float scale_l[QD_CH];
+    __shared__ float xsum_l[QD_CH];
+
+    const int lane = threadIdx.x & 63;
+    const int64_t wave_id = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t row0 = wave_id * rpw;
+    const int nrows = (int) (M - row0 < rpw ? (M - row0 > 0 ? M - row0 : 0) : rpw);
+
+    float acc[QD_RMAX];
+#pragma unroll
+    for (int r = 0; r < QD_RMAX; ++r) acc[r] = 0.f;
+
+    const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
+    uint32_t w[QD_RMAX][PW];
+    for (int64_t c = 0; c < nchunks; ++c) {
+        const int64_t cb = nblk - c * QD_CH < QD_CH ? nblk - c * QD_CH : QD_CH;
+        const bool mine = nrows > 0 && 2 * lane < cb;  // this lane owns a pair of this chunk
+        const uint8_t* base = W + row0 * nb1_w + (c * QD_CH + 2 * lane) * BYTES;
+        auto issue = [&](int r) {
+            if (mine && r < nrows) {
+                const uint32_t* p32 = (const uint32_t*) (base + r * nb1_w);
+#pragma unroll
+                for (int i = 0; i < PW; ++i) w[r][i] = p32[i];
+            }
+        };
+        // x is loaded first (vector loads return in issue order), then the
+        // weight stream starts so that it overlaps the conversion of x
+        f4 xv[4];
+        qd_load_x(x + c * QD_CH * QK, cb, xv);
+#pragma unroll
+        for (int r = 0; r < QD_PREFETCH; ++r) issue(r);
+        if (c > 0) __syncthreads();  // previous chunk's planes are no longer read
+        qd_prologue(xv, cb, planes, scale_l, xsum_l);
+        __syncthreads();
+        if (!mine) continue;
+
+        // this lane's pair: planes of blocks A (groups 0-7) and B (groups 8-15)
+        uint32_t PA[3][8], PB[3][8];
+        const uint32_t* src = planes + lane * QD_PSTRIDE;
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint4 v = *(const uint4*) (src + 16 * p + 4 * g);
+                uint32_t* dst = g < 2 ? &PA[p][4 * g] : &PB[p][4 * (g - 2)];
+                dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+            }
+        }
+        const float sc[2] = {scale_l[2 * lane], scale_l[2 * lane + 1]};
+        const float xs[2] = {xsum_l[2 * lane], xsum_l[2 * lane + 1]};
+#pragma unroll
+        for (int r = 0; r < QD_RMAX; ++r) {
+            if (r + QD_PREFETCH < QD_RMAX) issue(r + QD_PREFETCH);
+            if (r < nrows) acc[r] += qd_pair<TYPE>(w[r], PA, PB, sc, xs);
+        }
+    }
+    if (nrows == 0) return;
+#pragma unroll
+    for (int r = 0; r < QD_RMAX; ++r) acc[r] = wave_sum_lane63(acc[r]);
+    if (lane == 63) {
+#pragma unroll
+        for (int r = 0; r < QD_RMAX; ++r) {
+            if (r < nrows) y[row0 + r] = acc[r];
+        }
+    }
+}
+
+int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+        cus = 256;
+    }
+    return cus;
+}
+
+template <int TYPE>
+int launch_qmatvec_dot(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y,
+                       hipStream_t s) {
+    // spread the rows evenly over 8 waves per CU (2 per SIMD), at most QD_RMAX each
+    const int64_t target_waves = (int64_t) device_cus() * 8;
+    int64_t rpw = (M + target_waves - 1) / target_waves;
+    if (rpw > QD_RMAX) rpw = QD_RMAX;
+    if (rpw < 1) rpw = 1;
+    const int64_t waves = (M + rpw - 1) / rpw;
+    const int64_t grid = (waves + 3) / 4;
+    hipLaunchKernelGGL((k_qmatvec_dot<TYPE>), dim3((unsigned) grid), dim3(256), 0, s, (const uint8_t*) wq, nblk, M,
+                       (int64_t) nb1_w, x, y, (int) rpw);
+    return check_launch("qmatvec_dot");
+}
+
+int qv1_grid(int64_t M, int rows) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+        cus = 256;
+    }
+    const int64_t tiles = (M + rows - 1) / rows;
+    const int64_t want = (tiles + QV1_WAVES - 1) / QV1_WAVES;
+    const int64_t cap = (int64_t) cus * 2;
+    return (int) (want < cap ? want : cap);
+}
+
 template <int TYPE, int NB, int R>
 int launch_nb(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N, size_t nb1_x, float* y,
               size_t nb1_y, hipStream_t stream) {
@@ -183,6 +733,22 @@ int launch_nb(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x
 template <int TYPE>
 int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N, size_t nb1_x,
                 float* y, size_t nb1_y, hipStream_t s) {
+    const int64_t nblk = K / QK;
+    // N = 1 integer-dot kernel: pairs of blocks start on 4-byte boundaries
+    if constexpr (TYPE != TRC_HIP_TYPE_Q8_0) {
+        if (N == 1 && nblk % 2 == 0 && (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0 &&
+            (((uintptr_t) x) & 15u) == 0) {
+            return launch_qmatvec_dot<TYPE>(wq, nblk, M, nb1_w, x, y, s);
+        }
+    }
+    // N = 1 streaming kernel: needs 16-byte aligned rows and row chunks
+    if (N == 1 && nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0) {
+        // Q8_0 blocks are twice as large: a 4-row tile already fills the registers.
+        constexpr int ROWS = TYPE == TRC_HIP_TYPE_Q8_0 ? 4 : 8;
+        hipLaunchKernelGGL((k_qmatvec_n1<TYPE, ROWS, 4>), dim3(qv1_grid(M, ROWS)), dim3(QV1_WAVES * 64), 0, s,
+                           (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, y);
+        return check_launch("qmatvec_n1");
+    }
     if (N == 1) return launch_nb<TYPE, 1, 4>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s);
     if (N == 2) return launch_nb<TYPE, 2, 4>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s);
     if (N <= 4) return launch_nb<TYPE, 4, 2>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s);
