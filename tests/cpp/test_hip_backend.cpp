@@ -1,0 +1,574 @@
+// Drop-in tests of the HIP backend through the traincpp API (libtraincpp_hip.so),
+// modelled on the reference's backend conformance suite
+// (tests/test_backend_conformance.cpp:43-135, 455-553, 928-934) and its GGUF
+// tests (tests/test_gguf.cpp). Expected values come from the CPU oracle
+// (oracle/liboracle.so), which restates the reference CPU path.
+//
+//   test_hip_backend            all cases (needs a HIP device)
+//   test_hip_backend --cpu      only the cases that need no device
+//   test_hip_backend --abort-shape   builds an invalid mul_mat (must abort)
+#include "traincpp/traincpp.h"
+#include "oracle.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <utility>
+#include <vector>
+
+using namespace traincpp;
+
+namespace {
+
+int g_failures = 0;
+
+#define EXPECT(cond)                                                                  \
+    do {                                                                              \
+        if (!(cond)) {                                                                \
+            std::printf("    FAILED %s:%d: %s\n", __FILE__, __LINE__, #cond);          \
+            ++g_failures;                                                             \
+        }                                                                             \
+    } while (0)
+
+std::vector<float> ramp(size_t n) {  // tests/test_backend_conformance.cpp:130-135
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = (float) ((int) (i % 17) - 8) * 0.25f;
+    return v;
+}
+
+std::vector<float> normal(size_t n, uint64_t seed, float stddev = 1.0f) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; ++i) {
+        uint64_t s = seed + i;
+        v[i] = orc_rng_normal(&s, 0.0f, stddev);
+    }
+    return v;
+}
+
+// max over dst rows of max|got - want| / ||want_row||_2
+double row_l2_error(const std::vector<float>& got, const std::vector<float>& want, int64_t row) {
+    double worst = 0;
+    for (size_t r0 = 0; r0 < want.size(); r0 += (size_t) row) {
+        double n2 = 0, mx = 0;
+        for (int64_t i = 0; i < row; ++i) {
+            n2 += (double) want[r0 + i] * want[r0 + i];
+            mx = std::fmax(mx, std::fabs((double) got[r0 + i] - want[r0 + i]));
+        }
+        worst = std::fmax(worst, mx / std::fmax(std::sqrt(n2), 1e-30));
+    }
+    return worst;
+}
+
+// Host copies of the inputs of a graph, to rebuild any view's host pointer.
+struct HostInputs {
+    std::vector<std::pair<Tensor*, std::vector<float>>> f32;
+    const float* host_of(const Tensor* view) const {
+        const Tensor* root = view;
+        while (root->view_src) root = root->view_src;
+        for (const auto& p : f32) {
+            if (p.first == root) return (const float*) ((const uint8_t*) p.second.data() + (view->data_offset - root->data_offset));
+        }
+        return nullptr;
+    }
+};
+
+std::vector<float> oracle_mul_mat(const HostInputs& in, const Tensor* a, const Tensor* b) {
+    const int64_t dne[4] = {a->ne[1], b->ne[1], b->ne[2], b->ne[3]};
+    const size_t dnb[4] = {4, (size_t) (4 * dne[0]), (size_t) (4 * dne[0] * dne[1]), (size_t) (4 * dne[0] * dne[1] * dne[2])};
+    std::vector<float> out((size_t) (dne[0] * dne[1] * dne[2] * dne[3]));
+    const int rc = orc_mul_mat(in.host_of(a), a->ne, a->nb, in.host_of(b), b->ne, b->nb, out.data(), dne, dnb, 8);
+    EXPECT(rc == 0);
+    return out;
+}
+
+struct Built {
+    Tensor* out = nullptr;
+    HostInputs inputs;
+};
+
+using BuildFn = std::function<Built(Context*)>;
+
+// Runs a graph on `dev` and returns its output (and the built graph's inputs).
+std::vector<float> run_on(Device* dev, const BuildFn& build, Built* keep, const Tensor** first_bad = nullptr) {
+    Context* ctx = context_new(1 << 20);
+    Graph* g = graph_new(ctx);
+    Built b = build(ctx);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    EXPECT(buf != nullptr && buf->base() == nullptr && !buf->is_host());
+    for (auto& in : b.inputs.f32) tensor_set(in.first, in.second.data(), 0, in.second.size() * sizeof(float));
+    graph_build_forward_expand(ctx, g, b.out);
+    std::vector<float> out;
+    const Tensor* bad = graph_first_unsupported(g, dev);
+    if (first_bad) *first_bad = bad;
+    if (bad == nullptr) {
+        EXPECT(dev->graph_compute(g));
+        out.resize((size_t) tensor_nelements(b.out));
+        tensor_get(b.out, out.data(), 0, out.size() * sizeof(float));
+    }
+    if (keep) {
+        // keep the mul_mat node's source views valid for the oracle: recompute here
+        *keep = b;
+        keep->out = nullptr;
+    }
+    // oracle on the same views, before the context is released
+    if (keep && b.out->op == OP_MUL_MAT) {
+        std::vector<float> want = oracle_mul_mat(b.inputs, b.out->src[0], b.out->src[1]);
+        keep->inputs.f32.push_back({nullptr, std::move(want)});
+    }
+    buffer_free(buf);
+    graph_free(g);
+    context_free(ctx);
+    return out;
+}
+
+void check_mul_mat_case(Device* dev, const char* name, const BuildFn& build) {
+    Built kept;
+    const std::vector<float> got = run_on(dev, build, &kept);
+    const std::vector<float>& want = kept.inputs.f32.back().second;
+    EXPECT(got.size() == want.size());
+    if (got.size() != want.size()) return;
+    int64_t bad = 0;
+    double max_abs = 0;
+    for (size_t i = 0; i < want.size(); ++i) {
+        const double d = std::fabs((double) got[i] - want[i]);
+        max_abs = std::fmax(max_abs, d);
+        if (d > 1e-5 + 2e-4 * std::fabs((double) want[i])) ++bad;  // test_backend_conformance.cpp:107
+    }
+    EXPECT(bad == 0);
+    std::printf("    [%s] %-28s max_abs=%.3g\n", bad == 0 ? " OK " : "FAIL", name, max_abs);
+}
+
+Tensor* input(Built& b, Tensor* t, std::vector<float> v) {
+    b.inputs.f32.push_back({t, std::move(v)});
+    return t;
+}
+
+// ---------------------------------------------------------------- device cases
+
+void test_registry(Device* dev) {
+    std::printf("registry\n");
+    EXPECT(device_count() >= 1);
+    EXPECT(device_by_type(DeviceType::GPU) == dev);
+    EXPECT(device_cpu() == nullptr);
+    EXPECT(hip_device(hip_device_count()) == nullptr);
+    const DeviceProps& p = dev->props();
+    EXPECT(p.type == DeviceType::GPU && p.memory_total > 0);
+    std::printf("    %s: %s, %.1f GiB\n", p.name.c_str(), p.description.c_str(), p.memory_total / 1073741824.0);
+    EXPECT(dev->default_buffer_type()->alignment() >= 16);
+    EXPECT(dev->default_buffer_type()->alloc_buffer((size_t) 1 << 52) == nullptr);  // 4 PiB: refused, no abort
+}
+
+void test_conformance_mul_mat(Device* dev) {
+    std::printf("conformance mul_mat (tests/test_backend_conformance.cpp:455-553,928-934)\n");
+    check_mul_mat_case(dev, "mul_mat_basic", [](Context* ctx) {
+        Built b;
+        Tensor* x = input(b, new_tensor_2d(ctx, TYPE_F32, 5, 3), ramp(15));
+        Tensor* y = input(b, new_tensor_2d(ctx, TYPE_F32, 5, 4), ramp(20));
+        b.out = mul_mat(ctx, x, y);
+        return b;
+    });
+    check_mul_mat_case(dev, "mul_mat_transposed_a", [](Context* ctx) {
+        Built b;
+        Tensor* base = input(b, new_tensor_2d(ctx, TYPE_F32, 3, 5), ramp(15));
+        Tensor* y = input(b, new_tensor_2d(ctx, TYPE_F32, 5, 4), ramp(20));
+        b.out = mul_mat(ctx, transpose(ctx, base), y);
+        return b;
+    });
+    check_mul_mat_case(dev, "mul_mat_transposed_b", [](Context* ctx) {
+        Built b;
+        Tensor* x = input(b, new_tensor_2d(ctx, TYPE_F32, 5, 3), ramp(15));
+        Tensor* base = input(b, new_tensor_2d(ctx, TYPE_F32, 4, 5), ramp(20));
+        b.out = mul_mat(ctx, x, transpose(ctx, base));
+        return b;
+    });
+    check_mul_mat_case(dev, "mul_mat_tile_boundary", [](Context* ctx) {
+        Built b;
+        Tensor* x = input(b, new_tensor_2d(ctx, TYPE_F32, 33, 70), ramp(33 * 70));
+        Tensor* y = input(b, new_tensor_2d(ctx, TYPE_F32, 33, 66), ramp(33 * 66));
+        b.out = mul_mat(ctx, x, y);
+        return b;
+    });
+    check_mul_mat_case(dev, "mul_mat_batch", [](Context* ctx) {
+        Built b;
+        Tensor* x = input(b, new_tensor_4d(ctx, TYPE_F32, 5, 3, 1, 1), ramp(15));
+        Tensor* y = input(b, new_tensor_4d(ctx, TYPE_F32, 5, 4, 2, 3), ramp(5 * 4 * 6));
+        b.out = mul_mat(ctx, x, y);
+        return b;
+    });
+    check_mul_mat_case(dev, "mul_mat_batch_bcast_div", [](Context* ctx) {
+        Built b;
+        Tensor* x = input(b, new_tensor_4d(ctx, TYPE_F32, 5, 3, 2, 1), ramp(30));
+        Tensor* y = input(b, new_tensor_4d(ctx, TYPE_F32, 5, 4, 4, 1), ramp(80));
+        b.out = mul_mat(ctx, x, y);
+        return b;
+    });
+    check_mul_mat_case(dev, "mul_mat_batch_transposed", [](Context* ctx) {
+        Built b;
+        Tensor* xa = input(b, new_tensor_4d(ctx, TYPE_F32, 3, 5, 2, 2), ramp(60));
+        Tensor* xb = input(b, new_tensor_4d(ctx, TYPE_F32, 4, 5, 2, 2), ramp(80));
+        b.out = mul_mat(ctx, transpose(ctx, xa), transpose(ctx, xb));
+        return b;
+    });
+    check_mul_mat_case(dev, "mul_mat_batch_tile_boundary", [](Context* ctx) {
+        Built b;
+        Tensor* x = input(b, new_tensor_4d(ctx, TYPE_F32, 33, 70, 1, 1), ramp(33 * 70));
+        Tensor* y = input(b, new_tensor_4d(ctx, TYPE_F32, 33, 66, 2, 2), ramp(33 * 66 * 4));
+        b.out = mul_mat(ctx, x, y);
+        return b;
+    });
+    check_mul_mat_case(dev, "grid_mul_mat_batch_z", [](Context* ctx) {
+        Built b;
+        Tensor* x = input(b, new_tensor_4d(ctx, TYPE_F32, 8, 4, 1, 1), ramp(32));
+        Tensor* y = input(b, new_tensor_4d(ctx, TYPE_F32, 8, 4, 65, 1), ramp(8 * 4 * 65));
+        b.out = mul_mat(ctx, x, y);
+        return b;
+    });
+    check_mul_mat_case(dev, "permuted_src1_broadcast", [](Context* ctx) {  // configuration 4 in miniature
+        Built b;
+        Tensor* x = input(b, new_tensor_4d(ctx, TYPE_F32, 32, 40, 2, 2), normal(32 * 40 * 4, 11));
+        Tensor* base = input(b, new_tensor_4d(ctx, TYPE_F32, 32, 6, 24, 2), normal(32 * 6 * 24 * 2, 12));
+        b.out = mul_mat(ctx, x, permute(ctx, base, 0, 2, 1, 3));
+        return b;
+    });
+}
+
+// Linear layer y = W x and the two products autograd emits for it
+// (src/core/trc_autograd.cpp:487-503), with the transposed dW materialised by cont.
+void test_linear_backward(Device* dev) {
+    std::printf("linear layer forward + backward compositions\n");
+    const int64_t K = 256, M = 192, T = 64;
+    const std::vector<float> W = normal((size_t) (K * M), 1), X = normal((size_t) (K * T), 2),
+                             dY = normal((size_t) (M * T), 3, 1e-2f);
+    Context* ctx = context_new(1 << 20);
+    Tensor* w = new_tensor_2d(ctx, TYPE_F32, K, M);
+    Tensor* x = new_tensor_2d(ctx, TYPE_F32, K, T);
+    Tensor* dy = new_tensor_2d(ctx, TYPE_F32, M, T);
+    Tensor* y = mul_mat(ctx, w, x);
+    Tensor* dx = mul_mat(ctx, transpose(ctx, w), dy);
+    Tensor* dwt = mul_mat(ctx, transpose(ctx, dy), transpose(ctx, x));  // [M, K] = dW^T
+    Tensor* dw = cont(ctx, transpose(ctx, dwt));                       // [K, M] like W
+    Graph* g = graph_new(ctx);
+    graph_build_forward_expand(ctx, g, y);
+    graph_build_forward_expand(ctx, g, dx);
+    graph_build_forward_expand(ctx, g, dw);
+    EXPECT(graph_first_unsupported(g, dev) == nullptr);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    tensor_set(w, W.data(), 0, W.size() * 4);
+    tensor_set(x, X.data(), 0, X.size() * 4);
+    tensor_set(dy, dY.data(), 0, dY.size() * 4);
+    EXPECT(dev->graph_compute(g));
+    std::vector<float> gy((size_t) (M * T)), gdx((size_t) (K * T)), gdw((size_t) (K * M));
+    tensor_get(y, gy.data(), 0, gy.size() * 4);
+    tensor_get(dx, gdx.data(), 0, gdx.size() * 4);
+    tensor_get(dw, gdw.data(), 0, gdw.size() * 4);
+    // oracle: same views on host
+    HostInputs in;
+    in.f32 = {{w, W}, {x, X}, {dy, dY}};
+    const std::vector<float> wy = oracle_mul_mat(in, y->src[0], y->src[1]);
+    const std::vector<float> wdx = oracle_mul_mat(in, dx->src[0], dx->src[1]);
+    const std::vector<float> wdwt = oracle_mul_mat(in, dwt->src[0], dwt->src[1]);
+    std::vector<float> wdw((size_t) (K * M));
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t k = 0; k < K; ++k) wdw[(size_t) (m * K + k)] = wdwt[(size_t) (k * M + m)];
+    const double ey = row_l2_error(gy, wy, M), edx = row_l2_error(gdx, wdx, K), edw = row_l2_error(gdw, wdw, K);
+    EXPECT(ey <= 1e-4 && edx <= 1e-4 && edw <= 1e-4);
+    std::printf("    [%s] y err %.2e, dX err %.2e, dW (cont of transposed product) err %.2e\n",
+                (ey <= 1e-4 && edx <= 1e-4 && edw <= 1e-4) ? " OK " : "FAIL", ey, edx, edw);
+    buffer_free(buf);
+    graph_free(g);
+    context_free(ctx);
+}
+
+// ---------------------------------------------------------------- GGUF
+
+void put(std::vector<uint8_t>& v, const void* p, size_t n) {
+    v.insert(v.end(), (const uint8_t*) p, (const uint8_t*) p + n);
+}
+template <typename T>
+void put(std::vector<uint8_t>& v, T x) {
+    put(v, &x, sizeof(T));
+}
+
+// One-tensor GGUF v3 file in the reference test's byte layout (tests/test_gguf.cpp:58-107).
+bool write_gguf(const std::string& path, const char* name, Type type, const std::vector<int64_t>& ne,
+                const std::vector<uint8_t>& data, bool with_kv = true) {
+    std::vector<uint8_t> f;
+    put(f, "GGUF", 4);
+    put<uint32_t>(f, 3);
+    put<uint64_t>(f, 1);
+    put<uint64_t>(f, with_kv ? 1 : 0);
+    if (with_kv) {
+        const std::string key = "general.architecture", val = "hip-test";
+        put<uint64_t>(f, key.size());
+        put(f, key.data(), key.size());
+        put<int32_t>(f, (int32_t) GgufType::STRING);
+        put<uint64_t>(f, val.size());
+        put(f, val.data(), val.size());
+    }
+    const size_t nl = std::strlen(name);
+    put<uint64_t>(f, nl);
+    put(f, name, nl);
+    put<uint32_t>(f, (uint32_t) ne.size());
+    for (int64_t d : ne) put<int64_t>(f, d);
+    put<uint32_t>(f, (uint32_t) type);
+    put<uint64_t>(f, 0);
+    while (f.size() % 32) f.push_back(0);
+    put(f, data.data(), data.size());
+    while (f.size() % 32) f.push_back(0);
+    FILE* fp = std::fopen(path.c_str(), "wb");
+    if (!fp) return false;
+    const bool ok = std::fwrite(f.data(), 1, f.size(), fp) == f.size();
+    std::fclose(fp);
+    return ok;
+}
+
+// Seeded quant blocks: d ~ U[2e-4, 1e-3] as fp16, random payload bytes.
+std::vector<uint8_t> quant_blocks(Type type, int64_t n_blocks, uint64_t seed) {
+    const size_t bb = type_size(type);
+    std::vector<uint8_t> v((size_t) n_blocks * bb);
+    for (int64_t b = 0; b < n_blocks; ++b) {
+        uint64_t s = seed + (uint64_t) b;
+        uint8_t* blk = v.data() + (size_t) b * bb;
+        const uint16_t d = orc_fp32_to_fp16(2e-4f + (1e-3f - 2e-4f) * orc_rng_uniform01(&s));
+        std::memcpy(blk, &d, 2);
+        for (size_t i = 2; i < bb; i += 8) {
+            const uint64_t r = orc_rng_next_u64(&s);
+            std::memcpy(blk + i, &r, std::min<size_t>(8, bb - i));
+        }
+        if (type == TYPE_Q4_1 || type == TYPE_Q5_1) {
+            const uint16_t m = orc_fp32_to_fp16(-0.05f * orc_rng_uniform01(&s));
+            std::memcpy(blk + 2, &m, 2);
+        }
+    }
+    return v;
+}
+
+std::vector<float> oracle_dequant(Type type, const std::vector<uint8_t>& blocks) {
+    const int64_t n = (int64_t) (blocks.size() / type_size(type));
+    std::vector<float> out((size_t) n * 32);
+    EXPECT(orc_dequant((int) type, blocks.data(), n, out.data(), 8) == 0);
+    return out;
+}
+
+// Configuration 0: a Q8_0 4096x4096 weight in a GGUF file, loaded through the
+// reader with dequantization to F32 on the GPU, then mul_mat with X [4096, 8].
+void test_gguf_config0(Device* dev, const std::string& dir) {
+    std::printf("GGUF warm start (configuration 0)\n");
+    const int64_t K = 4096, M = 4096, N = 8;
+    const std::vector<uint8_t> blocks = quant_blocks(TYPE_Q8_0, K * M / 32, 0x7261696E);
+    const std::string path = dir + "/cfg0_q8_0.gguf";
+    EXPECT(write_gguf(path, "blk.0.ffn.weight", TYPE_Q8_0, {K, M}, blocks));
+    EXPECT(gguf_validate(path.c_str()));
+    GgufFile* f = gguf_open(path.c_str(), true);
+    EXPECT(f != nullptr);
+    if (!f) return;
+    EXPECT(gguf_version(f) == 3 && gguf_tensor_count(f) == 1);
+    EXPECT(std::string(gguf_get_str(f, "general.architecture")) == "hip-test");
+    Context* ctx = context_new(1 << 20);
+    Tensor* w = gguf_new_tensor(ctx, f, "blk.0.ffn.weight", TYPE_F32);
+    Tensor* x = new_tensor_2d(ctx, TYPE_F32, K, N);
+    Tensor* y = mul_mat(ctx, w, x);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    EXPECT(gguf_load_tensor(f, "blk.0.ffn.weight", w));
+    const std::vector<float> X = normal((size_t) (K * N), 5);
+    tensor_set(x, X.data(), 0, X.size() * 4);
+    std::vector<float> wf((size_t) (K * M));
+    tensor_get(w, wf.data(), 0, wf.size() * 4);
+    const std::vector<float> want_w = oracle_dequant(TYPE_Q8_0, blocks);
+    const bool exact = std::memcmp(wf.data(), want_w.data(), wf.size() * 4) == 0;
+    EXPECT(exact);
+    Graph* g = graph_new(ctx);
+    graph_build_forward_expand(ctx, g, y);
+    EXPECT(dev->graph_compute(g));
+    std::vector<float> gy((size_t) (M * N));
+    tensor_get(y, gy.data(), 0, gy.size() * 4);
+    HostInputs in;
+    in.f32 = {{w, want_w}, {x, X}};
+    const double e = row_l2_error(gy, oracle_mul_mat(in, w, x), M);
+    EXPECT(e <= 1e-4);
+    std::printf("    [%s] load+dequant on GPU bit-exact: %s; mul_mat err %.2e\n", (exact && e <= 1e-4) ? " OK " : "FAIL",
+                exact ? "yes" : "NO", e);
+    // gguf_tensor_to_f32 (host output) goes through the GPU as well
+    std::vector<float> host((size_t) (K * M));
+    EXPECT(gguf_tensor_to_f32(f, "blk.0.ffn.weight", host.data(), (int64_t) host.size()));
+    EXPECT(std::memcmp(host.data(), want_w.data(), host.size() * 4) == 0);
+    buffer_free(buf);
+    graph_free(g);
+    context_free(ctx);
+    gguf_close(f);
+    std::remove(path.c_str());
+}
+
+// Quantized tensors inside graphs: raw blocks loaded as Q4_0/Q5_0/..., then
+// cast to F32 (dequant node) and mul_mat with F32 activations (fused kernel
+// for N <= 16, dequantize + MFMA otherwise).
+void test_quantized_graph(Device* dev, const std::string& dir) {
+    std::printf("quantized tensors in graphs\n");
+    const Type types[] = {TYPE_Q4_0, TYPE_Q4_1, TYPE_Q5_0, TYPE_Q5_1, TYPE_Q8_0};
+    const int64_t K = 512, M = 96;
+    for (Type qt : types) {
+        for (int64_t N : {1, 5, 16, 40}) {
+            const std::vector<uint8_t> blocks = quant_blocks(qt, K * M / 32, 77 + (uint64_t) qt);
+            const std::string path = dir + "/q_" + type_name(qt) + ".gguf";
+            EXPECT(write_gguf(path, "w", qt, {K, M}, blocks, false));
+            GgufFile* f = gguf_open(path.c_str(), true);
+            EXPECT(f != nullptr);
+            if (!f) continue;
+            Context* ctx = context_new(1 << 20);
+            Tensor* wq = gguf_new_tensor(ctx, f, "w", qt);
+            Tensor* x = new_tensor_2d(ctx, TYPE_F32, K, N);
+            Tensor* y = mul_mat(ctx, wq, x);
+            Tensor* wf = cast(ctx, wq, TYPE_F32);
+            Graph* g = graph_new(ctx);
+            graph_build_forward_expand(ctx, g, y);
+            graph_build_forward_expand(ctx, g, wf);
+            EXPECT(graph_first_unsupported(g, dev) == nullptr);
+            Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+            EXPECT(gguf_load_tensor(f, "w", wq));  // same type: raw upload
+            const std::vector<float> X = normal((size_t) (K * N), 9 + (uint64_t) N);
+            tensor_set(x, X.data(), 0, X.size() * 4);
+            EXPECT(dev->graph_compute(g));
+            std::vector<float> gy((size_t) (M * N)), gw((size_t) (K * M));
+            tensor_get(y, gy.data(), 0, gy.size() * 4);
+            tensor_get(wf, gw.data(), 0, gw.size() * 4);
+            const std::vector<float> want_w = oracle_dequant(qt, blocks);
+            const bool exact = std::memcmp(gw.data(), want_w.data(), gw.size() * 4) == 0;
+            HostInputs in;  // oracle: mul_mat on the (bit-exact) dequantized weights
+            in.f32 = {{wf, want_w}, {x, X}};
+            const double e = row_l2_error(gy, oracle_mul_mat(in, wf, x), M);
+            EXPECT(exact && e <= 1e-4);
+            std::printf("    [%s] %-5s N=%-3lld cast bit-exact: %s, mul_mat err %.2e\n", (exact && e <= 1e-4) ? " OK " : "FAIL",
+                        type_name(qt), (long long) N, exact ? "yes" : "NO", e);
+            buffer_free(buf);
+            graph_free(g);
+            context_free(ctx);
+            gguf_close(f);
+            std::remove(path.c_str());
+        }
+    }
+}
+
+void test_fill_and_unsupported(Device* dev) {
+    std::printf("fill_tensors / supports_op\n");
+    Context* ctx = context_new(1 << 16);
+    Tensor* a = new_tensor_2d(ctx, TYPE_F32, 1000, 3);
+    Tensor* b = new_tensor_1d(ctx, TYPE_F32, 17);
+    Tensor* h = new_tensor_2d(ctx, TYPE_F16, 8, 8);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    TensorFill fills[2] = {{a, 1.5f}, {b, -3.0f}};
+    tensor_fill_values(fills, 2);
+    std::vector<float> va(3000), vb(17);
+    tensor_get(a, va.data(), 0, va.size() * 4);
+    tensor_get(b, vb.data(), 0, vb.size() * 4);
+    bool ok = true;
+    for (float v : va) ok = ok && v == 1.5f;
+    for (float v : vb) ok = ok && v == -3.0f;
+    EXPECT(ok);
+    // nodes the backend does not implement are reported, not run
+    Tensor* add_node = new_tensor_2d(ctx, TYPE_F32, 1000, 3);
+    add_node->op = OP_ADD;
+    add_node->src[0] = a;
+    add_node->src[1] = a;
+    add_node->nsrc = 2;
+    EXPECT(!dev->supports_op(add_node));
+    Tensor* hh = mul_mat(ctx, h, h);  // F16 mul_mat: not on this backend
+    EXPECT(!dev->supports_op(hh));
+    Graph* g = graph_new(ctx);
+    graph_build_forward_expand(ctx, g, add_node);
+    EXPECT(graph_first_unsupported(g, dev) == add_node);
+    std::printf("    [%s] fill + unsupported-op reporting\n", ok ? " OK " : "FAIL");
+    buffer_free(buf);
+    EXPECT(a->data == nullptr && a->buffer == nullptr);  // buffer_free detaches its tensors
+    graph_free(g);
+    context_free(ctx);
+}
+
+// ---------------------------------------------------------------- device-free cases
+
+void test_core_cpu(const std::string& dir) {
+    std::printf("core (no device)\n");
+    Context* ctx = context_new(1 << 16);
+    Tensor* a = new_tensor_4d(ctx, TYPE_F32, 6, 5, 4, 3);
+    EXPECT(a->nb[0] == 4 && a->nb[1] == 24 && a->nb[2] == 120 && a->nb[3] == 480);
+    Tensor* p = permute(ctx, a, 0, 2, 1, 3);  // ne[i] = a.ne[axes[i]]
+    EXPECT(p->ne[1] == 4 && p->ne[2] == 5 && p->nb[1] == 120 && p->nb[2] == 24 && !tensor_is_contiguous(p));
+    Tensor* t = transpose(ctx, a);
+    EXPECT(t->ne[0] == 5 && t->ne[1] == 6 && t->nb[0] == 24 && t->nb[1] == 4);
+    EXPECT(cont(ctx, a) == a && cont(ctx, t) != t && cont(ctx, t)->op == OP_CONT);
+    Tensor* q = new_tensor_2d(ctx, TYPE_Q4_0, 64, 3);
+    EXPECT(q->nb[0] == 18 && q->nb[1] == 36 && tensor_nbytes(q) == 108);
+    Tensor* x = new_tensor_2d(ctx, TYPE_F32, 64, 2);
+    Tensor* y = mul_mat(ctx, q, x);
+    EXPECT(y->type == TYPE_F32 && y->ne[0] == 3 && y->ne[1] == 2);
+    Graph* g = graph_new(ctx);
+    graph_build_forward_expand(ctx, g, y);
+    EXPECT(graph_n_nodes(g) == 3 && graph_node(g, 2) == y && graph_n_leafs(g) == 2);
+    EXPECT(std::string(op_name(OP_MUL_MAT)) == "mul_mat" && std::string(op_name(OP_WEIGHTNORM_SYNC)) == "weightnorm_sync");
+    EXPECT(std::string(type_name(TYPE_Q5_1)) == "q5_1" && type_size(TYPE_Q8_0) == 34 && type_blck_size(TYPE_Q4_1) == 32);
+    graph_free(g);
+    context_free(ctx);
+
+    // GGUF metadata parse and corrupt-file rejection (tests/test_gguf.cpp:526-635)
+    const std::vector<uint8_t> blocks = quant_blocks(TYPE_Q4_0, 4, 3);
+    const std::string ok_path = dir + "/ok.gguf";
+    EXPECT(write_gguf(ok_path, "w", TYPE_Q4_0, {128}, blocks));
+    GgufFile* f = gguf_open(ok_path.c_str(), false);
+    EXPECT(f != nullptr && gguf_tensor_count(f) == 1 && gguf_tensor_info(f, 0)->nbytes == 72);
+    std::vector<float> out(128);
+    EXPECT(!gguf_tensor_to_f32(f, "w", out.data(), 128));  // opened without data
+    gguf_close(f);
+    const std::string bad_ne0 = dir + "/bad_ne0.gguf";  // Q4_0 with ne0 = 30 (test_gguf.cpp:613-619)
+    EXPECT(write_gguf(bad_ne0, "w", TYPE_Q4_0, {30}, std::vector<uint8_t>(18)));
+    EXPECT(gguf_open(bad_ne0.c_str(), true) == nullptr);
+    const std::string bad_magic = dir + "/bad_magic.gguf";
+    FILE* fp = std::fopen(bad_magic.c_str(), "wb");
+    std::fwrite("GGUX\3\0\0\0", 1, 8, fp);
+    std::fclose(fp);
+    EXPECT(gguf_open(bad_magic.c_str(), true) == nullptr);
+    const std::string trunc = dir + "/trunc.gguf";
+    {
+        std::vector<uint8_t> v;
+        put(v, "GGUF", 4);
+        put<uint32_t>(v, 3);
+        put<uint64_t>(v, 1);
+        put<uint64_t>(v, 0);
+        FILE* tp = std::fopen(trunc.c_str(), "wb");
+        std::fwrite(v.data(), 1, v.size(), tp);
+        std::fclose(tp);
+    }
+    EXPECT(gguf_open(trunc.c_str(), true) == nullptr);
+    for (const std::string& s : {ok_path, bad_ne0, bad_magic, trunc}) std::remove(s.c_str());
+    std::printf("    [%s] layout, views, graph order, GGUF parsing\n", g_failures == 0 ? " OK " : "FAIL");
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const std::string mode = argc > 1 ? argv[1] : "";
+    const char* tmp = std::getenv("TMPDIR");
+    const std::string dir = tmp ? tmp : "/tmp";
+    if (mode == "--abort-shape") {  // death test: inner dimensions differ -> abort
+        Context* ctx = context_new(1 << 16);
+        mul_mat(ctx, new_tensor_2d(ctx, TYPE_F32, 4, 2), new_tensor_2d(ctx, TYPE_F32, 5, 2));
+        return 0;
+    }
+    test_core_cpu(dir);
+    if (mode != "--cpu") {
+        Device* dev = device_by_type(DeviceType::GPU);
+        if (dev == nullptr) {
+            std::printf("no HIP device\n");
+            return 2;
+        }
+        test_registry(dev);
+        test_conformance_mul_mat(dev);
+        test_linear_backward(dev);
+        test_gguf_config0(dev, dir);
+        test_quantized_graph(dev, dir);
+        test_fill_and_unsupported(dev);
+    }
+    std::printf("%s: %d failure(s)\n", g_failures == 0 ? "PASS" : "FAIL", g_failures);
+    return g_failures == 0 ? 0 : 1;
+}

@@ -1,0 +1,403 @@
+// MI355X HIP backend for traincpp: Device / BufferType / Buffer over the C ABI
+// of libtrc_hip.so (include/trc_hip_abi.h).
+//
+// It plugs into the reference's backend interface (include/traincpp/trc_backend.h:33-88)
+// the way its Vulkan backend does for a non-host device
+// (src/backends/vulkan/trc_vulkan.cpp:761-948): buffers are device memory
+// (base() == nullptr, tensors addressed as buffer + Tensor::data_offset),
+// set_tensor/get_tensor copy synchronously, graph_compute enqueues one kernel
+// per node on the null stream and waits once at the end, and any device error
+// aborts with a diagnostic. This file uses only the public traincpp API and
+// the C ABI, so it compiles against the reference's own headers as well.
+#include "traincpp/traincpp.h"
+#include "trc_hip_abi.h"
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace traincpp {
+
+namespace {
+
+[[noreturn]] void hip_abort(const char* what, int code) {
+    std::fflush(stdout);
+    std::fprintf(stderr, "[traincpp-hip][FATAL] %s failed (status %d): %s\n", what, code, trc_hip_last_error());
+    std::fflush(stderr);
+    std::abort();
+}
+
+void check(int code, const char* what) {
+    if (code != TRC_HIP_OK) hip_abort(what, code);
+}
+
+bool legacy_quant(Type t) {
+    return t == TYPE_Q4_0 || t == TYPE_Q4_1 || t == TYPE_Q5_0 || t == TYPE_Q5_1 || t == TYPE_Q8_0;
+}
+
+size_t elem_size(Type t) {
+    switch (t) {
+        case TYPE_F32: case TYPE_I32: return 4;
+        case TYPE_F16: case TYPE_BF16: case TYPE_I16: return 2;
+        case TYPE_I8: return 1;
+        case TYPE_F64: case TYPE_I64: return 8;
+        default: return 0;
+    }
+}
+
+const Tensor* storage_root(const Tensor* t) {
+    while (t->buffer == nullptr && t->view_src != nullptr) t = t->view_src;
+    return t;
+}
+
+class HipDevice;
+
+class HipBufferType final : public BufferType {
+public:
+    explicit HipBufferType(HipDevice* dev, int ordinal) : dev_(dev), name_("HIP" + std::to_string(ordinal)) {}
+    Device* device() const override;
+    const char* name() const override { return name_.c_str(); }
+    size_t alignment() const override { return 256; }
+    Buffer* alloc_buffer(size_t size) override;
+
+private:
+    HipDevice* dev_;
+    std::string name_;
+};
+
+class HipBuffer final : public Buffer {
+public:
+    HipBuffer(HipBufferType* bt, int ordinal, uint8_t* dev, size_t size)
+        : bt_(bt), ordinal_(ordinal), dev_(dev), size_(size) {}
+    ~HipBuffer() override {
+        trc_hip_init(ordinal_, nullptr);
+        trc_hip_free(dev_);
+    }
+    BufferType* buffer_type() const override { return bt_; }
+    size_t size() const override { return size_; }
+    void* base() override { return nullptr; }
+    bool is_host() const override { return false; }
+
+    void set_tensor(Tensor* t, size_t offset, const void* data, size_t size) override {
+        check(trc_hip_init(ordinal_, nullptr), "select device");
+        check(trc_hip_h2d(address(t) + offset, data, size, nullptr), "Buffer::set_tensor");
+    }
+    void get_tensor(const Tensor* t, size_t offset, void* data, size_t size) const override {
+        check(trc_hip_init(ordinal_, nullptr), "select device");
+        check(trc_hip_d2h(data, address(t) + offset, size, nullptr), "Buffer::get_tensor");
+    }
+    void clear() override {
+        check(trc_hip_init(ordinal_, nullptr), "select device");
+        check(trc_hip_memset(dev_, 0, size_, nullptr), "Buffer::clear");
+        check(trc_hip_sync(nullptr), "Buffer::clear");
+    }
+
+    uint8_t* address(const Tensor* t) const {
+        if (t->data_offset + tensor_nbytes(t) > size_) {
+            std::fprintf(stderr, "[traincpp-hip][FATAL] tensor %s lies outside its buffer\n", t->name);
+            std::abort();
+        }
+        return dev_ + t->data_offset;
+    }
+    int ordinal() const { return ordinal_; }
+
+private:
+    HipBufferType* bt_;
+    int ordinal_;
+    uint8_t* dev_;
+    size_t size_;
+};
+
+HipBuffer* hip_buffer_of(const Tensor* t) {
+    return dynamic_cast<HipBuffer*>(storage_root(t)->buffer);
+}
+
+trc_hip_tensor describe(const Tensor* t, const HipBuffer* b) {
+    trc_hip_tensor d;
+    std::memset(&d, 0, sizeof(d));
+    d.data = b->address(t);
+    d.type = (int32_t) t->type;
+    for (int i = 0; i < 4; ++i) {
+        d.ne[i] = t->ne[i];
+        d.nb[i] = t->nb[i];
+    }
+    return d;
+}
+
+class HipDevice final : public Device {
+public:
+    explicit HipDevice(int ordinal) : ordinal_(ordinal), buft_(this, ordinal) {
+        trc_hip_props p;
+        check(trc_hip_init(ordinal, &p), "trc_hip_init");
+        props_.name = "HIP" + std::to_string(ordinal);
+        props_.description = std::string(p.name) + " (" + p.arch + ", " + std::to_string(p.compute_units) + " CUs)";
+        props_.type = DeviceType::GPU;
+        props_.memory_free = p.memory_free;
+        props_.memory_total = p.memory_total;
+        props_.unified_memory = p.unified_memory != 0;
+    }
+
+    const DeviceProps& props() const override { return props_; }
+    BufferType* default_buffer_type() override { return &buft_; }
+
+    bool supports_op(const Tensor* t) const override {
+        const Tensor* a = t->src[0];
+        const Tensor* b = t->src[1];
+        switch (t->op) {
+            case OP_NONE:
+            case OP_VIEW:
+            case OP_RESHAPE:
+            case OP_PERMUTE:
+            case OP_TRANSPOSE:
+                return true;
+            case OP_DUP:
+            case OP_CPY:
+            case OP_CONT:
+                return a != nullptr && a->type == t->type && elem_size(t->type) != 0;
+            case OP_CAST:  // dequantization of a legacy quant tensor
+                return a != nullptr && legacy_quant(a->type) && t->type == TYPE_F32 && tensor_is_contiguous(a) &&
+                       tensor_is_contiguous(t);
+            case OP_MUL_MAT: {
+                if (a == nullptr || b == nullptr || t->type != TYPE_F32 || b->type != TYPE_F32) return false;
+                if (a->ne[0] != b->ne[0] || b->ne[2] % a->ne[2] != 0 || b->ne[3] % a->ne[3] != 0) return false;
+                if (a->type == TYPE_F32) return true;
+                // quantized src0: whole rows of blocks, activations contiguous along k
+                return legacy_quant(a->type) && a->nb[0] == type_size(a->type) && b->nb[0] == sizeof(float) &&
+                       t->nb[0] == sizeof(float);
+            }
+            default:
+                return false;
+        }
+    }
+
+    bool graph_compute(Graph* graph) override {
+        select();
+        for (Tensor* node : graph->nodes) compute(node);
+        check(trc_hip_sync(nullptr), "graph_compute");
+        return true;
+    }
+
+    bool fill_tensors(const TensorFill* fills, size_t count) override {
+        select();
+        for (size_t i = 0; i < count; ++i) {
+            Tensor* t = fills[i].tensor;
+            HipBuffer* buf = hip_buffer_of(t);
+            if (buf == nullptr || t->type != TYPE_F32 || !tensor_is_contiguous(t)) {
+                if (!Device::fill_tensors(&fills[i], 1)) return false;
+                continue;
+            }
+            check(trc_hip_fill_f32((float*) buf->address(t), fills[i].value, tensor_nelements(t), nullptr),
+                  "fill_tensors");
+        }
+        check(trc_hip_sync(nullptr), "fill_tensors");
+        return true;
+    }
+
+    void select() const { check(trc_hip_init(ordinal_, nullptr), "select device"); }
+    int ordinal() const { return ordinal_; }
+
+    // Device scratch that grows on demand (released with the device).
+    uint8_t* scratch(size_t bytes) {
+        if (bytes > scratch_size_) {
+            if (scratch_ != nullptr) {
+                check(trc_hip_sync(nullptr), "scratch");
+                trc_hip_free(scratch_);
+                scratch_ = nullptr;
+            }
+            void* p = nullptr;
+            check(trc_hip_malloc(&p, bytes), "scratch allocation");
+            scratch_ = (uint8_t*) p;
+            scratch_size_ = bytes;
+        }
+        return scratch_;
+    }
+
+private:
+    [[noreturn]] void unsupported(const Tensor* t) const {
+        std::fflush(stdout);
+        std::fprintf(stderr,
+                     "[traincpp-hip][FATAL] HIP backend cannot compute node %s (op %s, type %s); check the graph with "
+                     "graph_first_unsupported() before graph_compute()\n",
+                     t->name, op_name(t->op), type_name(t->type));
+        std::abort();
+    }
+
+    HipBuffer* need_buffer(const Tensor* t) const {
+        HipBuffer* b = hip_buffer_of(t);
+        if (b == nullptr) {
+            std::fprintf(stderr, "[traincpp-hip][FATAL] tensor %s is not in a HIP buffer\n", t->name);
+            std::abort();
+        }
+        return b;
+    }
+
+    void compute(Tensor* t) {
+        if (!supports_op(t)) unsupported(t);
+        switch (t->op) {
+            case OP_NONE: case OP_VIEW: case OP_RESHAPE: case OP_PERMUTE: case OP_TRANSPOSE:
+                return;
+            case OP_DUP: case OP_CPY: case OP_CONT: {
+                const trc_hip_tensor s = describe(t->src[0], need_buffer(t->src[0]));
+                const trc_hip_tensor d = describe(t, need_buffer(t));
+                check(trc_hip_cpy(&s, &d, nullptr), op_name(t->op));
+                return;
+            }
+            case OP_CAST: {
+                const Tensor* a = t->src[0];
+                check(trc_hip_dequant((int) a->type, need_buffer(a)->address(a), tensor_nelements(a) / 32,
+                                      (float*) need_buffer(t)->address(t), nullptr),
+                      "cast (dequantize)");
+                return;
+            }
+            case OP_MUL_MAT:
+                if (t->src[0]->type == TYPE_F32) {
+                    const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
+                    const trc_hip_tensor b = describe(t->src[1], need_buffer(t->src[1]));
+                    const trc_hip_tensor d = describe(t, need_buffer(t));
+                    check(trc_hip_mul_mat_f32(&a, &b, &d, nullptr), "mul_mat");
+                } else {
+                    mul_mat_quant(t);
+                }
+                return;
+            default:
+                unsupported(t);
+        }
+    }
+
+    // mul_mat with a legacy quant src0: the fused kernel for skinny right-hand
+    // sides, otherwise the planes of src0 are dequantized into scratch and the
+    // FP32 MFMA kernel runs on them.
+    void mul_mat_quant(Tensor* t) {
+        const Tensor* a = t->src[0];
+        const Tensor* b = t->src[1];
+        uint8_t* pa = need_buffer(a)->address(a);
+        uint8_t* pb = need_buffer(b)->address(b);
+        uint8_t* pd = need_buffer(t)->address(t);
+        const int64_t K = a->ne[0], M = a->ne[1], N = b->ne[1];
+        if (N <= TRC_HIP_QMATVEC_MAX_N) {
+            for (int64_t i3 = 0; i3 < b->ne[3]; ++i3) {
+                for (int64_t i2 = 0; i2 < b->ne[2]; ++i2) {
+                    const uint8_t* wa = pa + (i2 % a->ne[2]) * a->nb[2] + (i3 % a->ne[3]) * a->nb[3];
+                    const float* xb = (const float*) (pb + i2 * b->nb[2] + i3 * b->nb[3]);
+                    float* yd = (float*) (pd + i2 * t->nb[2] + i3 * t->nb[3]);
+                    check(trc_hip_qmatvec((int) a->type, wa, K, M, a->nb[1], xb, N, b->nb[1], yd, t->nb[1], nullptr),
+                          "mul_mat (fused quantized matvec)");
+                }
+            }
+            return;
+        }
+        const int64_t planes = a->ne[2] * a->ne[3];
+        const size_t plane_f32 = (size_t) (K * M) * sizeof(float);
+        float* wf = (float*) scratch(plane_f32 * (size_t) planes);
+        const size_t row_bytes = (size_t) (K / 32) * type_size(a->type);
+        for (int64_t p3 = 0; p3 < a->ne[3]; ++p3) {
+            for (int64_t p2 = 0; p2 < a->ne[2]; ++p2) {
+                const uint8_t* src = pa + p2 * a->nb[2] + p3 * a->nb[3];
+                float* dst = wf + (p2 + p3 * a->ne[2]) * K * M;
+                if (a->nb[1] == row_bytes) {
+                    check(trc_hip_dequant((int) a->type, src, K * M / 32, dst, nullptr), "mul_mat (dequantize src0)");
+                } else {
+                    for (int64_t r = 0; r < M; ++r) {
+                        check(trc_hip_dequant((int) a->type, src + r * a->nb[1], K / 32, dst + r * K, nullptr),
+                              "mul_mat (dequantize src0)");
+                    }
+                }
+            }
+        }
+        trc_hip_tensor af;
+        std::memset(&af, 0, sizeof(af));
+        af.data = wf;
+        af.type = TRC_HIP_TYPE_F32;
+        const int64_t ne[4] = {K, M, a->ne[2], a->ne[3]};
+        size_t nb = sizeof(float);
+        for (int i = 0; i < 4; ++i) {
+            af.ne[i] = ne[i];
+            af.nb[i] = nb;
+            nb *= (size_t) ne[i];
+        }
+        const trc_hip_tensor bd = describe(b, need_buffer(b));
+        const trc_hip_tensor dd = describe(t, need_buffer(t));
+        check(trc_hip_mul_mat_f32(&af, &bd, &dd, nullptr), "mul_mat (dequantized src0)");
+    }
+
+    int ordinal_;
+    HipBufferType buft_;
+    DeviceProps props_;
+    uint8_t* scratch_ = nullptr;
+    size_t scratch_size_ = 0;
+};
+
+Device* HipBufferType::device() const {
+    return dev_;
+}
+
+Buffer* HipBufferType::alloc_buffer(size_t size) {
+    HipDevice* d = dev_;
+    d->select();
+    void* p = nullptr;
+    if (trc_hip_malloc(&p, size == 0 ? 256 : size) != TRC_HIP_OK) return nullptr;
+    return new HipBuffer(this, d->ordinal(), (uint8_t*) p, size == 0 ? 256 : size);
+}
+
+std::mutex g_devices_mutex;
+std::vector<std::unique_ptr<HipDevice>>& devices() {
+    static std::vector<std::unique_ptr<HipDevice>> v;
+    return v;
+}
+
+}  // namespace
+
+int hip_device_count() {
+    int n = 0;
+    if (trc_hip_device_count(&n) != TRC_HIP_OK) return 0;
+    return n;
+}
+
+Device* hip_device(int ordinal) {
+    std::lock_guard<std::mutex> lock(g_devices_mutex);
+    const int n = hip_device_count();
+    if (ordinal < 0 || ordinal >= n) return nullptr;
+    auto& v = devices();
+    if ((int) v.size() < n) v.resize((size_t) n);
+    if (!v[(size_t) ordinal]) v[(size_t) ordinal] = std::make_unique<HipDevice>(ordinal);
+    return v[(size_t) ordinal].get();
+}
+
+// ---- hooks used by the GGUF reader (core/hip_hooks.h) ----
+
+bool hip_dequant_into(Tensor* dst, Type type, const void* host_blocks, int64_t n_blocks) {
+    HipBuffer* buf = hip_buffer_of(dst);
+    if (buf == nullptr) return false;
+    HipDevice* dev = static_cast<HipDevice*>(buf->buffer_type()->device());
+    dev->select();
+    const size_t raw = (size_t) n_blocks * type_size(type);
+    uint8_t* staging = dev->scratch(raw);
+    check(trc_hip_h2d(staging, host_blocks, raw, nullptr), "gguf_load_tensor (upload blocks)");
+    check(trc_hip_dequant((int) type, staging, n_blocks, (float*) buf->address(dst), nullptr),
+          "gguf_load_tensor (dequantize)");
+    check(trc_hip_sync(nullptr), "gguf_load_tensor");
+    return true;
+}
+
+bool hip_dequant_host(Type type, const void* host_blocks, int64_t n_blocks, float* out) {
+    Device* d = hip_device(0);
+    if (d == nullptr) return false;
+    HipDevice* dev = static_cast<HipDevice*>(d);
+    dev->select();
+    const size_t raw = (size_t) n_blocks * type_size(type);
+    const size_t raw_aligned = (raw + 255) / 256 * 256;
+    uint8_t* s = dev->scratch(raw_aligned + (size_t) n_blocks * 32 * sizeof(float));
+    check(trc_hip_h2d(s, host_blocks, raw, nullptr), "gguf_tensor_to_f32 (upload blocks)");
+    check(trc_hip_dequant((int) type, s, n_blocks, (float*) (s + raw_aligned), nullptr),
+          "gguf_tensor_to_f32 (dequantize)");
+    check(trc_hip_d2h(out, s + raw_aligned, (size_t) n_blocks * 32 * sizeof(float), nullptr),
+          "gguf_tensor_to_f32 (download)");
+    return true;
+}
+
+}  // namespace traincpp

@@ -23,6 +23,9 @@ int hip_status(hipError_t e, const char* what) {
     if (e == hipSuccess) return TRC_HIP_OK;
     std::snprintf(g_last_error, sizeof(g_last_error), "%s: %s (hipError_t %d)", what,
                   hipGetErrorString(e), (int) e);
+    // The runtime also keeps the failure as its "last error"; clear it so that
+    // the launch check of a later kernel does not report this stale error.
+    (void) hipGetLastError();
     return (int) e;
 }
 
@@ -101,7 +104,7 @@ int trc_hip_init(int ordinal, trc_hip_props* props) {
     st = hip_status(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
     if (st != TRC_HIP_OK) return st;
     std::memset(props, 0, sizeof(*props));
-    std::snprintf(props->name, sizeof(props->name), "%s", p.name);
+    std::snprintf(props->name, sizeof(props->name), "%s", p.name[0] ? p.name : "AMD GPU");
     std::snprintf(props->arch, sizeof(props->arch), "%s", p.gcnArchName);
     props->ordinal = ordinal;
     props->compute_units = p.multiProcessorCount;
