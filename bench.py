@@ -285,6 +285,22 @@ def read_traffic():
         return None
 
 
+def copy_calibration(H, timer, steps, warmup):
+    """A plain device copy of a known size (256 MiB read + 256 MiB written) through
+    trc_hip_cpy: the reference point that scales the HBM traffic counters."""
+    n = 64 << 20  # floats
+    src = H.DeviceBuffer(n * 4)
+    dst = H.DeviceBuffer(n * 4)
+    H.fill_f32(src.ptr, 1.0, n)
+    a = H.tensor(src.ptr, [n, 1, 1, 1], H.contiguous_nb([n, 1, 1, 1]))
+    b = H.tensor(dst.ptr, [n, 1, 1, 1], H.contiguous_nb([n, 1, 1, 1]))
+    ms, mode = timer.run(lambda i, s: H.cpy(a, b, s), steps, warmup)
+    src.free()
+    dst.free()
+    return {"bytes_read": n * 4, "bytes_written": n * 4, "ms": ms, "GB/s": 2 * n * 4 / (ms * 1e-3) / 1e9,
+            "timing": mode}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -293,6 +309,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only time a 256 MiB device copy (reference for the traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; multi-GPU runs are not part of this "
@@ -306,6 +324,9 @@ def main():
     hip = Hip()
     timer = Timer(hip, use_graph=not args.no_graph)
     K, M = 4096, 14336
+    if args.calibrate_copy:
+        print(json.dumps({"calibration": "copy", **copy_calibration(H, timer, args.steps, args.warmup)}), flush=True)
+        return
 
     t_wall = time.perf_counter()
     head, blk, x = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 1, args.steps, args.warmup)
