@@ -94,3 +94,105 @@ def test_argument_errors(hip):
     with pytest.raises(H.HipError) as e:
         H.qmatvec(H.TYPE_Q4_1, w.ptr + 2, 64, 4, 40, x.ptr, 1, 256, y.ptr, 16)
     assert e.value.code == H.E_ALIGN
+
+
+# The int8 matrix-core kernel (qmm.hip) takes 2 <= N <= 16 with an even
+# number of blocks per row; the cases below pin its layouts, grid shapes and
+# numerics. Odd block counts above exercise the fallback kernels.
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("N", [2, 3, 7, 16])
+def test_mfma_path_all_formats(hip, name, N):
+    t = TYPES[name]
+    K, M = 32 * 38, 301  # 19 pairs: uneven split over the waves; M not a tile multiple
+    announce(f"qmm {name} K={K} M={M} N={N}")
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 211 + t))
+    X = synth.normal(31 + N, K * N).reshape(1, 1, N, K)
+    got = gpu_qmatvec(t, raw, K, M, X)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert O.row_l2_error(got, want) <= TOL
+
+
+@pytest.mark.parametrize("name", ["q4_0", "q5_1", "q8_0"])
+@pytest.mark.parametrize("M", [1, 5, 16, 250, 3000, 20000])
+def test_mfma_grid_shapes(hip, name, M):
+    """Rows per workgroup from 8 to 64 (1 to 4 tiles), masked tail rows."""
+    t = TYPES[name]
+    K, N = 64 * 5, 16
+    announce(f"qmm grid {name} K={K} M={M}")
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 3 + M))
+    X = synth.normal(17 + M, K * N).reshape(1, 1, N, K)
+    got = gpu_qmatvec(t, raw, K, M, X, x_pad=8, y_pad=5)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert O.row_l2_error(got, want) <= TOL
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_mfma_dynamic_range(hip, name):
+    """Columns of very different magnitude, blocks of very different magnitude
+    inside one column, and denormal x: the scale is per block and column."""
+    t = TYPES[name]
+    K, M, N = 32 * 16, 96, 9
+    announce(f"qmm range {name}")
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 77 + t))
+    X = synth.normal(5, K * N).reshape(1, 1, N, K).astype(np.float32)
+    col_scale = np.array([1e-30, 1e-6, 1e-3, 1.0, 1e3, 1e6, 1e20, 3e25, 1.0], np.float32)
+    X *= col_scale[None, None, :, None]
+    X[0, 0, 8, 64:96] *= np.float32(1e12)  # one loud block in an otherwise unit column
+    X[0, 0, 8, 96:128] *= np.float32(1e-12)  # and a quiet one
+    X[0, 0, 3, 0:32] = np.float32(1e-40)  # a block of denormals next to normal blocks
+    got = gpu_qmatvec(t, raw, K, M, X)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert np.isfinite(got).all()
+    assert O.row_l2_error(got, want) <= TOL
+
+
+@pytest.mark.parametrize("name", ["q4_0", "q5_1", "q8_0"])
+@pytest.mark.parametrize("N", [1, 4])
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
+def test_nonfinite_x(hip, name, N, bad):
+    """A non-finite x element makes its column non-finite, as in the reference
+    (the fixed-point kernels return NaN there); the other columns are unaffected.
+    Covers the integer-dot (N = 1), streaming (Q8_0, N = 1) and int8 MFMA kernels."""
+    t = TYPES[name]
+    K, M = 256, 40
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 8))
+    X = synth.normal(9, K * N).reshape(1, 1, N, K)
+    j = N - 1
+    X[0, 0, j, 37] = bad
+    got = gpu_qmatvec(t, raw, K, M, X)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert not np.isfinite(want[0, 0, j]).any()
+    assert not np.isfinite(got[0, 0, j]).any()
+    keep = [c for c in range(N) if c != j]
+    if keep:
+        assert O.row_l2_error(got[:, :, keep], want[:, :, keep]) <= TOL
+
+
+def test_mfma_q8_0_minus_128(hip):
+    """GGUF Q8_0 quants may be -128 (the synthetic draws stop at -127)."""
+    t = TYPES["q8_0"]
+    K, M, N = 128, 48, 16
+    blocks = synth.quant_blocks(t, K * M // 32, 21)
+    qs = blocks["qs"].copy()
+    qs[::3, ::5] = -128
+    qs[1::7, :] = -128  # whole blocks at the extreme
+    blocks["qs"] = qs
+    raw = synth.block_bytes(blocks)
+    X = synth.normal(22, K * N).reshape(1, 1, N, K)
+    got = gpu_qmatvec(t, raw, K, M, X)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert O.row_l2_error(got, want) <= TOL
+
+
+@pytest.mark.parametrize("nblk", [2048, 2050])
+def test_mfma_block_limit(hip, nblk):
+    """2048 blocks per row is the int8 kernel's limit; 2050 takes the fallback."""
+    t = TYPES["q5_0"]
+    K, M, N = 32 * nblk, 24, 5
+    announce(f"qmm limit nblk={nblk}")
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, nblk))
+    X = synth.normal(nblk, K * N).reshape(1, 1, N, K)
+    got = gpu_qmatvec(t, raw, K, M, X)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert O.row_l2_error(got, want) <= TOL

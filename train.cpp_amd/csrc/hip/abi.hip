@@ -60,6 +60,18 @@ int check_launch(const char* what) {
     return hip_status(hipGetLastError(), what);
 }
 
+int device_cus() {
+    constexpr int MAX_DEV = 64;
+    static int cached[MAX_DEV] = {};  // 0 = not queried yet; a benign race stores the same value
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+    if (dev < MAX_DEV && cached[dev] > 0) return cached[dev];
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (dev < MAX_DEV) cached[dev] = cus;
+    return cus;
+}
+
 }  // namespace trc_hip
 
 using namespace trc_hip;

@@ -36,6 +36,8 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
 // Launch-side error reporting, implemented in abi.hip.
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Compute units of the current device (cached per device).
+int device_cus();
 
 // Kernel launchers (one per kernel family). They validate what the kernels
 // assume, enqueue on `stream` and return a trc_hip_status / hipError_t.
@@ -44,6 +46,11 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
                        hipStream_t stream);
 int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x,
                    int64_t N, size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream);
+// Fused quant x skinny GEMM on the int8 matrix cores for 2 <= N <= 16
+// (qmm.hip); qmm_supported says whether the shape and alignment fit it.
+bool qmm_supported(int64_t K, int64_t N, const void* wq, size_t nb1_w);
+int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
+               size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream);
 int launch_fill_f32(float* dst, float value, int64_t count, hipStream_t stream);
 int launch_cpy(const trc_hip_tensor& src, const trc_hip_tensor& dst, size_t elem_size,
                hipStream_t stream);

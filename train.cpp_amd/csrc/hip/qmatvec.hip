@@ -484,16 +484,20 @@ __device__ __forceinline__ void qd_prologue(const f4* v, int64_t cb, uint32_t* p
     const int b = t >> 1, h = t & 1;
     const bool active = b < cb;
     float mx = 0.f, sm = 0.f;
+    int bad = 0;  // fmaxf drops NaN, so non-finite values are flagged separately
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
         sm += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        bad |= !__builtin_isfinite(v[i].x) | !__builtin_isfinite(v[i].y) | !__builtin_isfinite(v[i].z) |
+               !__builtin_isfinite(v[i].w);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
     sm += __shfl_xor(sm, 1, 64);
+    bad |= __shfl_xor(bad, 1, 64);
+    const bool finite = bad == 0;
     // s = 22 - E with mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^22
-    const int s = mx > 0.f ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
-    const bool finite = __builtin_isfinite(mx);
+    const int s = (mx > 0.f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
     uint32_t P[3][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -683,15 +687,6 @@ __global__ __launch_bounds__(256) void k_qmatvec_dot(const uint8_t* __restrict__
     }
 }
 
-int device_cus() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
-        cus = 256;
-    }
-    return cus;
-}
-
 template <int TYPE>
 int launch_qmatvec_dot(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y,
                        hipStream_t s) {
@@ -708,11 +703,7 @@ int launch_qmatvec_dot(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, co
 }
 
 int qv1_grid(int64_t M, int rows) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
-        cus = 256;
-    }
+    const int cus = device_cus();
     const int64_t tiles = (M + rows - 1) / rows;
     const int64_t want = (tiles + QV1_WAVES - 1) / QV1_WAVES;
     const int64_t cap = (int64_t) cus * 2;
@@ -734,6 +725,8 @@ template <int TYPE>
 int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N, size_t nb1_x,
                 float* y, size_t nb1_y, hipStream_t s) {
     const int64_t nblk = K / QK;
+    // 2 <= N <= 16: int8 matrix-core kernel (qmm.hip)
+    if (qmm_supported(K, N, wq, nb1_w)) return launch_qmm(TYPE, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s);
     // N = 1 integer-dot kernel: pairs of blocks start on 4-byte boundaries
     if constexpr (TYPE != TRC_HIP_TYPE_Q8_0) {
         if (N == 1 && nblk % 2 == 0 && (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0 &&
