@@ -96,15 +96,16 @@ def test_argument_errors(hip):
     assert e.value.code == H.E_ALIGN
 
 
-# The int8 matrix-core kernel (qmm.hip) takes 2 <= N <= 16 with an even
-# number of blocks per row; the cases below pin its layouts, grid shapes and
-# numerics. Odd block counts above exercise the fallback kernels.
+# The int8 matrix-core kernel (qmm.hip) takes 2 <= N <= 16 with a multiple of
+# 8 blocks per row (K % 256 == 0), in chunks of 16 blocks; the cases below pin
+# its layouts, grid shapes, partial last chunks and numerics. Other block
+# counts above exercise the fallback kernels.
 
 @pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("N", [2, 3, 7, 16])
 def test_mfma_path_all_formats(hip, name, N):
     t = TYPES[name]
-    K, M = 32 * 38, 301  # 19 pairs: uneven split over the waves; M not a tile multiple
+    K, M = 32 * 40, 301  # 20 pairs: two full chunks and a half one; M not a tile multiple
     announce(f"qmm {name} K={K} M={M} N={N}")
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 211 + t))
     X = synth.normal(31 + N, K * N).reshape(1, 1, N, K)
@@ -118,7 +119,7 @@ def test_mfma_path_all_formats(hip, name, N):
 def test_mfma_grid_shapes(hip, name, M):
     """Rows per workgroup from 8 to 64 (1 to 4 tiles), masked tail rows."""
     t = TYPES[name]
-    K, N = 64 * 5, 16
+    K, N = 256 * 3, 16
     announce(f"qmm grid {name} K={K} M={M}")
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 3 + M))
     X = synth.normal(17 + M, K * N).reshape(1, 1, N, K)
@@ -172,7 +173,7 @@ def test_nonfinite_x(hip, name, N, bad):
 def test_mfma_q8_0_minus_128(hip):
     """GGUF Q8_0 quants may be -128 (the synthetic draws stop at -127)."""
     t = TYPES["q8_0"]
-    K, M, N = 128, 48, 16
+    K, M, N = 256, 48, 16
     blocks = synth.quant_blocks(t, K * M // 32, 21)
     qs = blocks["qs"].copy()
     qs[::3, ::5] = -128
@@ -185,9 +186,9 @@ def test_mfma_q8_0_minus_128(hip):
     assert O.row_l2_error(got, want) <= TOL
 
 
-@pytest.mark.parametrize("nblk", [2048, 2050])
+@pytest.mark.parametrize("nblk", [2048, 2056])
 def test_mfma_block_limit(hip, nblk):
-    """2048 blocks per row is the int8 kernel's limit; 2050 takes the fallback."""
+    """2048 blocks per row is the int8 kernel's limit; 2056 takes the fallback."""
     t = TYPES["q5_0"]
     K, M, N = 32 * nblk, 24, 5
     announce(f"qmm limit nblk={nblk}")

@@ -11,10 +11,12 @@
 // block b and column j, X_e = rint(x_e * 2^s) with s chosen so |X_e| <= 2^21,
 // i.e. 22 significant bits for the block's largest |x|. X is split into three
 // signed byte digits, X = P0 + 256 P1 + 65536 P2 (P0, P1 in [-128, 127],
-// |P2| <= 32). The three MFMAs per block then give the exact integer sums
-// sum_e q_e P_p,e; for Q4_0/Q4_1/Q5_0/Q5_1 they combine exactly into one
-// int32 (|q| <= 31 keeps it below 2^31), for Q8_0 in float. One conversion and
-// two float operations apply 2^-s and d. The only rounding beyond FP32's is
+// |P2| <= 32). The quants enter the MFMAs unsigned (0..31) or as int8 (Q8_0);
+// the Q4_0/Q5_0 bias goes into the first MFMA's accumulator input as
+// -bias * sum_e X_e. The three MFMAs per block then give exact integer sums
+// that combine into one int32 for Q4_0/Q4_1/Q5_0/Q5_1 (the exact result is
+// below 2^31 since |q - bias| <= 31), and in float for Q8_0. One conversion
+// and two float operations apply 2^-s and d. The only rounding beyond FP32's is
 // the 22-bit representation of x (at most 2^-22 of the block maximum per
 // element), the same order as the reference's own FP32 sum over 32 products.
 // A block of x holding Inf or NaN turns its columns' outputs into NaN.
@@ -34,7 +36,7 @@
 //
 // Work split: a workgroup owns up to 64 rows (T tiles of 16). Its QM_WAVES
 // waves split the K pairs evenly, and each wave streams its share of the
-// pairs of all T tiles with QM_DEPTH pairs of loads in flight. The partial
+// pairs of all T tiles with two pairs of loads in flight. The partial
 // sums are added across the waves through LDS in a fixed order, so results
 // are deterministic. Rows per workgroup are chosen so the grid covers every
 // CU once when M allows.
@@ -47,14 +49,17 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int QM_MAX_BLOCKS = 2048;  // K <= 65536
 constexpr int QM_WAVES = 8;
-constexpr int QM_DEPTH = 2;
+constexpr int QM_PLANES = 3;          // byte digits of x per element (2 would give 15-bit x: too coarse
+                                      // for the 1e-4 bar on short rows)
+constexpr int QM_XBITS = QM_PLANES == 3 ? 21 : 14;  // |X| <= 2^QM_XBITS
+constexpr uint32_t QM_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
 
 // x in block fixed point, written by k_qmm_xprep and read by k_qmm on the
-// same stream. Planes: [block][digit 0..2][lane 0..63] 8 bytes each; scale and
-// block sums: [block][column 0..15]. Calls that overlap on one GPU race.
-__device__ __attribute__((aligned(256))) uint64_t g_qm_planes[QM_MAX_BLOCKS * 3 * 64];
-__device__ __attribute__((aligned(256))) float g_qm_scale[QM_MAX_BLOCKS * 16];
-__device__ __attribute__((aligned(256))) float g_qm_xsum[QM_MAX_BLOCKS * 16];
+// same stream. Planes: [block][digit][lane 0..63] 8 bytes each. Meta:
+// [block][field][column 0..15] with fields 2^-s (f32), sum of x (f32) and
+// sum of X (i32). Calls that overlap on one GPU race.
+__device__ __attribute__((aligned(256))) uint64_t g_qm_planes[QM_MAX_BLOCKS * QM_PLANES * 64];
+__device__ __attribute__((aligned(256))) uint32_t g_qm_meta[QM_MAX_BLOCKS * 3 * 16];
 
 template <int TYPE>
 constexpr bool rotated_even() {
@@ -98,38 +103,49 @@ __global__ __launch_bounds__(256) void k_qmm_xprep(const float* __restrict__ x, 
     bad |= __shfl_xor(bad, 16, 64);
     bad |= __shfl_xor(bad, 32, 64);
     const bool finite = bad == 0;
-    // mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^21, so |X| <= 2^21
-    const int s = (mx > 0.f && finite) ? 21 - __builtin_amdgcn_frexp_expf(mx) : 0;
-    int d0[8], d1[8], d2[8];
+    // mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^QM_XBITS
+    const int s = (mx > 0.f && finite) ? QM_XBITS - __builtin_amdgcn_frexp_expf(mx) : 0;
+    int dg[QM_PLANES][8];
+    int sx = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int X = finite ? (int) __builtin_rintf(__builtin_ldexpf(v[i], s)) : 0;
+        sx += X;
         const int p0 = (int) (int8_t) (X & 0xFF);
         const int X1 = (X - p0) >> 8;
-        const int p1 = (int) (int8_t) (X1 & 0xFF);
-        d0[i] = p0;
-        d1[i] = p1;
-        d2[i] = (X1 - p1) >> 8;
+        dg[0][i] = p0;
+        if constexpr (QM_PLANES == 2) {
+            dg[1][i] = X1;  // |X1| <= 64
+        } else {
+            const int p1 = (int) (int8_t) (X1 & 0xFF);
+            dg[1][i] = p1;
+            dg[2][i] = (X1 - p1) >> 8;  // |.| <= 32
+        }
     }
-    uint64_t* dst = g_qm_planes + (int64_t) b * 3 * 64 + l;
-    dst[0] = (uint64_t) pack_bytes(d0) | ((uint64_t) pack_bytes(d0 + 4) << 32);
-    dst[64] = (uint64_t) pack_bytes(d1) | ((uint64_t) pack_bytes(d1 + 4) << 32);
-    dst[128] = (uint64_t) pack_bytes(d2) | ((uint64_t) pack_bytes(d2 + 4) << 32);
+    sx += __shfl_xor(sx, 16, 64);
+    sx += __shfl_xor(sx, 32, 64);
+    uint64_t* dst = g_qm_planes + (int64_t) b * QM_PLANES * 64 + l;
+#pragma unroll
+    for (int p = 0; p < QM_PLANES; ++p) {
+        dst[64 * p] = (uint64_t) pack_bytes(dg[p]) | ((uint64_t) pack_bytes(dg[p] + 4) << 32);
+    }
     if (g == 0) {
-        g_qm_scale[b * 16 + j] = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
-        g_qm_xsum[b * 16 + j] = sm;
+        uint32_t* meta = g_qm_meta + b * 48 + j;
+        meta[0] = __builtin_bit_cast(uint32_t, finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf(""));
+        meta[16] = __builtin_bit_cast(uint32_t, sm);
+        meta[32] = (uint32_t) sx;
     }
 }
 
-// Per format: which dwords of a pair each lane loads (NW of them) and how
-// they decode into the two blocks' B operands and scales.
+// Per format: which dwords of a pair each lane loads (NW of them), in bytes
+// from the pair start.
 template <int TYPE>
 struct QmFmt;
 
 // 9 dwords: [d0 qs0.0-1][qs0 2-5]..[qs0 14-15 d1][qs1 0-3]..[qs1 12-15]
 template <>
 struct QmFmt<TRC_HIP_TYPE_Q4_0> {
-    static constexpr int PW = 9, NW = 4;
+    static constexpr int PW = 9, NW = 4, BIAS = 8;
     __device__ static void offsets(int g, int* o) {
         o[0] = 0; o[1] = 4; o[2] = g < 3 ? 1 + g : 0; o[3] = 5 + g;
     }
@@ -137,7 +153,7 @@ struct QmFmt<TRC_HIP_TYPE_Q4_0> {
 // 10 dwords: [d0 m0][qs0 x4][d1 m1][qs1 x4]
 template <>
 struct QmFmt<TRC_HIP_TYPE_Q4_1> {
-    static constexpr int PW = 10, NW = 4;
+    static constexpr int PW = 10, NW = 4, BIAS = 0;
     __device__ static void offsets(int g, int* o) {
         o[0] = 0; o[1] = 5; o[2] = 1 + g; o[3] = 6 + g;
     }
@@ -145,7 +161,7 @@ struct QmFmt<TRC_HIP_TYPE_Q4_1> {
 // 11 dwords: [d0 qh0.lo][qh0.hi qs0.0-1][qs0 2-5]..[qs0 14-15 d1][qh1][qs1 x4]
 template <>
 struct QmFmt<TRC_HIP_TYPE_Q5_0> {
-    static constexpr int PW = 11, NW = 6;
+    static constexpr int PW = 11, NW = 6, BIAS = 16;
     __device__ static void offsets(int g, int* o) {
         o[0] = 0; o[1] = 1; o[2] = 5; o[3] = 6; o[4] = g < 3 ? 2 + g : 1; o[5] = 7 + g;
     }
@@ -153,7 +169,7 @@ struct QmFmt<TRC_HIP_TYPE_Q5_0> {
 // 12 dwords: [d0 m0][qh0][qs0 x4][d1 m1][qh1][qs1 x4]
 template <>
 struct QmFmt<TRC_HIP_TYPE_Q5_1> {
-    static constexpr int PW = 12, NW = 6;
+    static constexpr int PW = 12, NW = 6, BIAS = 0;
     __device__ static void offsets(int g, int* o) {
         o[0] = 0; o[1] = 1; o[2] = 6; o[3] = 7; o[4] = 2 + g; o[5] = 8 + g;
     }
@@ -161,7 +177,7 @@ struct QmFmt<TRC_HIP_TYPE_Q5_1> {
 // 17 dwords: [d0 qs0.0-1][qs0 2-5]..[qs0 30-31 d1][qs1 0-3]..[qs1 28-31]
 template <>
 struct QmFmt<TRC_HIP_TYPE_Q8_0> {
-    static constexpr int PW = 17, NW = 7;
+    static constexpr int PW = 17, NW = 7, BIAS = 0;
     __device__ static void offsets(int g, int* o) {
         o[0] = 0; o[1] = 4; o[2] = 8; o[3] = g < 3 ? 1 + g : 0; o[4] = g < 3 ? 5 + g : 4; o[5] = 9 + g;
         o[6] = 13 + g;
@@ -170,8 +186,9 @@ struct QmFmt<TRC_HIP_TYPE_Q8_0> {
 
 // Nibble bytes of a quant dword (low nibbles -> k 0..3, high -> k 4..7 of the
 // lane group), with the 5th bits of the 4 low / 4 high elements (bits 0-3 /
-// 4-7 of fifth) and the bias subtracted bytewise (no carries: values < 0x90).
-template <int BIAS, bool FIVE>
+// 4-7 of fifth). Values stay unsigned (0..31); a bias goes into the MFMA's
+// accumulator input instead.
+template <bool FIVE>
 __device__ __forceinline__ long nibbles(uint32_t w, uint32_t fifth) {
     uint32_t lo = w & 0x0F0F0F0Fu;
     uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
@@ -179,17 +196,10 @@ __device__ __forceinline__ long nibbles(uint32_t w, uint32_t fifth) {
         lo |= ((fifth & 0xFu) * 0x02040810u) & 0x10101010u;
         hi |= (((fifth >> 4) & 0xFu) * 0x02040810u) & 0x10101010u;
     }
-    if constexpr (BIAS == 8) {
-        lo = (lo + 0x78787878u) ^ 0x80808080u;
-        hi = (hi + 0x78787878u) ^ 0x80808080u;
-    } else if constexpr (BIAS == 16) {
-        lo = (lo + 0x70707070u) ^ 0x80808080u;
-        hi = (hi + 0x70707070u) ^ 0x80808080u;
-    }
     return (long) ((uint64_t) lo | ((uint64_t) hi << 32));
 }
 
-// 5th bits of lane group g's elements, from a block's qh rotated by c.
+// 5th bits of lane group g's elements, from a block's qh (rotated for c = 2).
 __device__ __forceinline__ uint32_t fifth_bits(uint32_t qh, int g) {
     return ((qh >> (4 * g)) & 0xFu) | (((qh >> (16 + 4 * g)) & 0xFu) << 4);
 }
@@ -206,24 +216,24 @@ template <int TYPE>
 __device__ __forceinline__ QmBlocks qm_decode(const uint32_t* w, int g, uint32_t sel) {
     QmBlocks r;
     if constexpr (TYPE == TRC_HIP_TYPE_Q4_0) {
-        r.B[0] = nibbles<8, false>(__builtin_amdgcn_perm(w[1], w[2], sel), 0);
-        r.B[1] = nibbles<8, false>(w[3], 0);
+        r.B[0] = nibbles<false>(__builtin_amdgcn_perm(w[1], w[2], sel), 0);
+        r.B[1] = nibbles<false>(w[3], 0);
         r.dm[0] = w[0] & 0xFFFFu;
         r.dm[1] = w[1] >> 16;
     } else if constexpr (TYPE == TRC_HIP_TYPE_Q4_1) {
-        r.B[0] = nibbles<0, false>(w[2], 0);
-        r.B[1] = nibbles<0, false>(w[3], 0);
+        r.B[0] = nibbles<false>(w[2], 0);
+        r.B[1] = nibbles<false>(w[3], 0);
         r.dm[0] = w[0];
         r.dm[1] = w[1];
     } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_0) {
         const uint32_t qh0 = __builtin_amdgcn_perm(w[1], w[0], 0x05040302u);
-        r.B[0] = nibbles<16, true>(__builtin_amdgcn_perm(w[2], w[4], sel), fifth_bits(rot2_halves(qh0), g));
-        r.B[1] = nibbles<16, true>(w[5], fifth_bits(w[3], g));
+        r.B[0] = nibbles<true>(__builtin_amdgcn_perm(w[2], w[4], sel), fifth_bits(rot2_halves(qh0), g));
+        r.B[1] = nibbles<true>(w[5], fifth_bits(w[3], g));
         r.dm[0] = w[0] & 0xFFFFu;
         r.dm[1] = w[2] >> 16;
     } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_1) {
-        r.B[0] = nibbles<0, true>(w[4], fifth_bits(w[1], g));
-        r.B[1] = nibbles<0, true>(w[5], fifth_bits(w[3], g));
+        r.B[0] = nibbles<true>(w[4], fifth_bits(w[1], g));
+        r.B[1] = nibbles<true>(w[5], fifth_bits(w[3], g));
         r.dm[0] = w[0];
         r.dm[1] = w[2];
     } else {  // Q8_0
@@ -237,122 +247,201 @@ __device__ __forceinline__ QmBlocks qm_decode(const uint32_t* w, int g, uint32_t
     return r;
 }
 
-template <int TYPE, int T>
-struct QmStage {
-    uint32_t w[T][QmFmt<TYPE>::NW];
-    long xp[2][3];
+constexpr int QM_CP = 8;       // pairs per K chunk (one per wave)
+constexpr int QM_RING = 3;     // chunks in flight: registers -> LDS ring depth
+
+// The x operands of one pair (two blocks) for this lane.
+struct QmX {
+    long xp[2][QM_PLANES];
     f4 sc[2];
-    f4 xs[2];
+    v4i aux[2];  // -BIAS * sum X (int) or the block sums of x (float bits)
 };
 
-template <int TYPE, int T>
-__device__ __forceinline__ void qm_load(QmStage<TYPE, T>& st, const uint32_t* const* rowp, const int* off, int p,
-                                        int lane, int g) {
-    constexpr int PW = QmFmt<TYPE>::PW, NW = QmFmt<TYPE>::NW;
+template <int TYPE>
+__device__ __forceinline__ void qm_load_x(QmX& x, __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rm, uint32_t xo,
+                                          uint32_t mo, int p) {
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
-    // x first: loads return in issue order and the x operands are needed first
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int b = 2 * p + h;
-        const uint64_t* xp = g_qm_planes + (int64_t) b * 3 * 64 + lane;
 #pragma unroll
-        for (int d = 0; d < 3; ++d) st.xp[h][d] = (long) xp[64 * d];
-        st.sc[h] = *(const f4*) (g_qm_scale + b * 16 + 4 * g);
-        if constexpr (MIN) st.xs[h] = *(const f4*) (g_qm_xsum + b * 16 + 4 * g);
-    }
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const uint32_t* src = rowp[t] + (int64_t) p * PW;
-#pragma unroll
-        for (int i = 0; i < NW; ++i) st.w[t][i] = src[off[i]];
+        for (int d = 0; d < QM_PLANES; ++d) {
+            x.xp[h][d] = __builtin_bit_cast(
+                long, __builtin_amdgcn_raw_buffer_load_b64(rx, xo, (b * QM_PLANES + d) * 512, 0));
+        }
+        x.sc[h] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, b * 192, 0));
+        if constexpr (MIN || QmFmt<TYPE>::BIAS != 0) {
+            x.aux[h] = __builtin_bit_cast(
+                v4i, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, b * 192 + (MIN ? 64 : 128), 0));
+        }
     }
 }
 
+// One pair of all T tiles: quant dwords from the LDS chunk, x from registers.
 template <int TYPE, int T>
-__device__ __forceinline__ void qm_compute(const QmStage<TYPE, T>& st, int g, uint32_t sel, f4* acc) {
+__device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32_t (*lo)[QmFmt<TYPE>::NW],
+                                           const QmX& x, int g, uint32_t sel, f4* acc) {
+    constexpr int NW = QmFmt<TYPE>::NW;
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
+    constexpr int BIAS = QmFmt<TYPE>::BIAS;
     const v4i zero = {0, 0, 0, 0};
+    v4i c0[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) c0[h] = BIAS != 0 ? x.aux[h] * (-BIAS) : zero;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        const QmBlocks q = qm_decode<TYPE>(st.w[t], g, sel);
+        uint32_t w[NW];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) w[i] = *(const uint32_t*) (lds_pair + lo[t][i]);
+        const QmBlocks q = qm_decode<TYPE>(w, g, sel);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const v4i a0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(st.xp[h][0], q.B[h], zero, 0, 0, 0);
-            const v4i a1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(st.xp[h][1], q.B[h], zero, 0, 0, 0);
-            const v4i a2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(st.xp[h][2], q.B[h], zero, 0, 0, 0);
+            // sum_e (q_e - BIAS) X_e = [sum_e q_e P0_e - BIAS sum_e X_e] + 256 sum_e q_e P1_e + 65536 sum_e q_e P2_e
+            const v4i a0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x.xp[h][0], q.B[h], c0[h], 0, 0, 0);
+            const v4i a1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x.xp[h][1], q.B[h], zero, 0, 0, 0);
+            v4i a2 = zero;
+            if constexpr (QM_PLANES == 3) a2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x.xp[h][2], q.B[h], zero, 0, 0, 0);
             const float d = half_bits_to_float(q.dm[h] & 0xFFFFu);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float qx;
-                if constexpr (TYPE == TRC_HIP_TYPE_Q8_0) {
+                if constexpr (QM_PLANES == 3 && TYPE == TRC_HIP_TYPE_Q8_0) {
                     qx = __builtin_fmaf((float) a2[i], 65536.f, (float) (a0[i] + a1[i] * 256));
+                } else if constexpr (QM_PLANES == 3) {
+                    // modulo 2^32: the exact result fits in int32 (|q - bias| <= 31, |X| <= 2^21)
+                    // even where the partial sums with the bias term would not
+                    qx = (float) (int) ((uint32_t) a0[i] + (uint32_t) a1[i] * 256u + (uint32_t) a2[i] * 65536u);
                 } else {
-                    qx = (float) (a0[i] + a1[i] * 256 + a2[i] * 65536);
+                    qx = (float) (int) ((uint32_t) a0[i] + (uint32_t) a1[i] * 256u);
                 }
-                acc[t][i] = __builtin_fmaf(qx, d * st.sc[h][i], acc[t][i]);
-                if constexpr (MIN) acc[t][i] = __builtin_fmaf(half_bits_to_float(q.dm[h] >> 16), st.xs[h][i], acc[t][i]);
+                acc[t][i] = __builtin_fmaf(qx, d * x.sc[h][i], acc[t][i]);
+                if constexpr (MIN) {
+                    // the element is copied out first: __builtin_bit_cast applied to a
+                    // vector-element lvalue reads element 0 with this compiler
+                    const int xs_bits = x.aux[h][i];
+                    acc[t][i] = __builtin_fmaf(half_bits_to_float(q.dm[h] >> 16), __builtin_bit_cast(float, xs_bits),
+                                               acc[t][i]);
+                }
             }
         }
     }
 }
+
+template <int TYPE, int T>
+struct QmTile {
+    static constexpr int PW = QmFmt<TYPE>::PW;
+    static constexpr int RB = QM_CP * PW * 4;         // bytes of one row in a chunk (a multiple of 16)
+    static constexpr int PITCH = RB + 16;             // LDS row pitch: rows start 4 banks apart
+    static constexpr int ROWS = 16 * T;
+    static constexpr int BUF = ROWS * PITCH;          // one chunk in LDS
+    static constexpr int PIECES = ROWS * (RB / 16);   // 16-byte pieces of a chunk
+    static constexpr int PPT = (PIECES + QM_WAVES * 64 - 1) / (QM_WAVES * 64);  // pieces per thread
+};
 
 template <int TYPE, int T>
 __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict__ W, int nblk, int64_t M,
                                                         int64_t nb1_w, float* __restrict__ y, int64_t ldy, int N,
                                                         int rows_per_wg) {
-    __shared__ f4 red[QM_WAVES][T][64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m16 = lane & 15, g = lane >> 4;
+    using TL = QmTile<TYPE, T>;
+    constexpr int NW = QmFmt<TYPE>::NW, PW = TL::PW;
+    static_assert(QM_RING * TL::BUF >= QM_WAVES * T * 64 * 16, "reduction buffer aliases the chunk ring");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[QM_RING * TL::BUF];
+
+    // wave index as a scalar: the pair a wave computes and its buffer offsets are wave-uniform
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, m16 = lane & 15, g = lane >> 4;
     const int64_t r0 = (int64_t) blockIdx.x * rows_per_wg;
     const int64_t rend = r0 + rows_per_wg < M ? r0 + rows_per_wg : M;
     const int np = nblk / 2;
-    const int p_begin = (int) ((int64_t) np * wave / QM_WAVES);
-    const int p_end = (int) ((int64_t) np * (wave + 1) / QM_WAVES);
+    const int nch = (np + QM_CP - 1) / QM_CP;
     const uint32_t sel = g < 3 ? 0x03020100u : 0x03020504u;
 
-    const uint32_t* rowp[T];
+    // The workgroup's rows as one buffer (the launcher keeps it below 2^31 bytes):
+    // loads of rows past M return zeros.
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void*) (W + r0 * nb1_w), (short) 0, (int) ((rend - r0) * nb1_w), QM_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void*) g_qm_planes, (short) 0, (int) sizeof(g_qm_planes), QM_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rm =
+        __builtin_amdgcn_make_buffer_rsrc((void*) g_qm_meta, (short) 0, (int) sizeof(g_qm_meta), QM_RSRC_WORD3);
+
+    // cooperative chunk copy: thread piece k -> row k / (RB/16), 16 bytes at (k % (RB/16)) * 16
+    uint32_t go[TL::PPT], so[TL::PPT];
+    bool pv[TL::PPT];
+#pragma unroll
+    for (int k = 0; k < TL::PPT; ++k) {
+        const int q = (int) threadIdx.x + k * QM_WAVES * 64;
+        const int row = q / (TL::RB / 16), pc = q % (TL::RB / 16);
+        pv[k] = q < TL::PIECES;
+        go[k] = (uint32_t) (row * nb1_w) + pc * 16;
+        so[k] = row * TL::PITCH + pc * 16;
+    }
+    // this lane's quant dwords of its wave's pair, per tile, as LDS byte offsets within a chunk
+    int off[NW];
+    QmFmt<TYPE>::offsets(g, off);
+    uint32_t lo[T][NW];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        const int64_t m = r0 + 16 * t + m16;
-        rowp[t] = (const uint32_t*) (W + (m < rend ? m : r0) * nb1_w);  // masked rows read row r0
+#pragma unroll
+        for (int i = 0; i < NW; ++i) lo[t][i] = (16 * t + m16) * TL::PITCH + wave * PW * 4 + 4 * off[i];
     }
-    int off[QmFmt<TYPE>::NW];
-    QmFmt<TYPE>::offsets(g, off);
+    const uint32_t xo = lane * 8, mo = 16 * g;
 
     f4 acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
-    if (p_begin < p_end) {
-        QmStage<TYPE, T> st[QM_DEPTH];
+    uint4 wr[QM_RING][TL::PPT];
+    QmX xr[QM_RING];
+    auto load_chunk = [&](int s, int c) {
+        const int cc = c < nch ? c : nch - 1;  // past the end: repeat the last chunk (unused)
 #pragma unroll
-        for (int d = 0; d < QM_DEPTH; ++d) {
-            const int p = p_begin + d < p_end ? p_begin + d : p_end - 1;
-            qm_load<TYPE, T>(st[d], rowp, off, p, lane, g);
-        }
-        int p = p_begin;
-        for (; p + QM_DEPTH <= p_end; p += QM_DEPTH) {
-#pragma unroll
-            for (int d = 0; d < QM_DEPTH; ++d) {
-                const QmStage<TYPE, T> cur = st[d];
-                const int pn = p + d + QM_DEPTH < p_end ? p + d + QM_DEPTH : p_end - 1;  // in bounds
-                qm_load<TYPE, T>(st[d], rowp, off, pn, lane, g);
-                qm_compute<TYPE, T>(cur, g, sel, acc);
+        for (int k = 0; k < TL::PPT; ++k) {
+            if (pv[k]) {
+                wr[s][k] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, go[k], cc * TL::RB, 0));
             }
         }
+        const int p = cc * QM_CP + wave;
+        qm_load_x<TYPE>(xr[s], rx, rm, xo, mo, p < np ? p : np - 1);
+    };
+    auto store_chunk = [&](int s, int buf) {
 #pragma unroll
-        for (int d = 0; d < QM_DEPTH; ++d) {
-            if (p + d < p_end) qm_compute<TYPE, T>(st[d], g, sel, acc);
+        for (int k = 0; k < TL::PPT; ++k) {
+            if (pv[k]) *(uint4*) (lds + buf * TL::BUF + so[k]) = wr[s][k];
         }
-    }
+    };
+    auto step = [&](int c, int s) {
+        // chunk c sits in LDS buffer s and its x in xr[s]; chunk c+1 goes to LDS, c+3 is fetched
+        if (c * QM_CP + wave < np) qm_compute<TYPE, T>(lds + s * TL::BUF, lo, xr[s], g, sel, acc);
+        store_chunk((s + 1) % QM_RING, (s + 1) % QM_RING);
+        load_chunk(s, c + QM_RING);
+        __syncthreads();
+    };
 
 #pragma unroll
-    for (int t = 0; t < T; ++t) red[wave][t][lane] = acc[t];
+    for (int s = 0; s < QM_RING; ++s) load_chunk(s, s);
+    store_chunk(0, 0);
+    __syncthreads();
+    int c = 0;
+    for (; c + QM_RING <= nch; c += QM_RING) {
+        step(c, 0);
+        step(c + 1, 1);
+        step(c + 2, 2);
+    }
+    if (c < nch) step(c, 0);
+    if (c + 1 < nch) step(c + 1, 1);
+
+    // sum over the waves (fixed order) through the now idle chunk ring
+    f4* red = (f4*) lds;
+#pragma unroll
+    for (int t = 0; t < T; ++t) red[(wave * T + t) * 64 + lane] = acc[t];
     __syncthreads();
     if (wave >= T) return;
     const int t = wave;
-    f4 sum = red[0][t][lane];
+    f4 sum = red[t * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < QM_WAVES; ++w) sum += red[w][t][lane];
+    for (int w = 1; w < QM_WAVES; ++w) sum += red[(w * T + t) * 64 + lane];
     const int64_t m = r0 + 16 * t + m16;
     if (m >= rend) return;
 #pragma unroll
@@ -396,8 +485,10 @@ int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x
 
 bool qmm_supported(int64_t K, int64_t N, const void* wq, size_t nb1_w) {
     const int64_t nblk = K / QK;
-    return N >= 2 && N <= 16 && nblk >= 2 && nblk % 2 == 0 && nblk <= QM_MAX_BLOCKS &&
-           (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0;
+    // K chunks are copied in 16-byte pieces (a multiple of 4 pairs per row keeps them
+    // aligned); a workgroup's 64 rows are addressed through one buffer resource (< 2^31 bytes)
+    return N >= 2 && N <= 16 && nblk >= 8 && nblk % 8 == 0 && nblk <= QM_MAX_BLOCKS &&
+           (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0 && nb1_w <= ((size_t) 1 << 24);
 }
 
 int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
