@@ -463,6 +463,8 @@ constexpr int QD_CH = 128;        // blocks per chunk of K (one lane = one pair)
 constexpr int QD_RMAX = 8;        // rows per wave at most
 constexpr int QD_PREFETCH = 3;    // rows whose loads are in flight
 constexpr int QD_PSTRIDE = 52;    // LDS dwords per pair of planes (48 + 4: conflict-free b128 reads)
+constexpr int QD_WAVES = 8;       // waves per workgroup: one x conversion serves 8 waves
+                                  // (the first 256 threads convert, the rest wait at the barrier)
 
 template <int TYPE>
 struct QdFmt {
@@ -613,52 +615,60 @@ __device__ __forceinline__ float wave_sum_lane63(float v) {
     return v;
 }
 
-template <int TYPE>
-__global__ __launch_bounds__(256) void k_qmatvec_dot(const uint8_t* __restrict__ W, int64_t nblk, int64_t M,
+template <int TYPE, int RPW>
+__global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __restrict__ W, int64_t nblk, int64_t M,
                                                      int64_t nb1_w, const float* __restrict__ x,
-                                                     float* __restrict__ y, int rpw) {
+                                                     float* __restrict__ y) {
     constexpr int BYTES = block_bytes(TYPE);
     constexpr int PW = QdFmt<TYPE>::PAIR_WORDS;
+    constexpr int PF = QD_PREFETCH < RPW ? QD_PREFETCH : RPW;
     __shared__ __attribute__((aligned(16))) uint32_t planes[(QD_CH / 2) * QD_PSTRIDE];
     __shared__ float scale_l[QD_CH];
     __shared__ float xsum_l[QD_CH];
 
     const int lane = threadIdx.x & 63;
-    const int64_t wave_id = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int64_t row0 = wave_id * rpw;
-    const int nrows = (int) (M - row0 < rpw ? (M - row0 > 0 ? M - row0 : 0) : rpw);
+    const int64_t wave_id = (int64_t) blockIdx.x * QD_WAVES + (threadIdx.x >> 6);
+    const int64_t row0 = wave_id * RPW;
 
-    float acc[QD_RMAX];
+    // No branches around loads and uses: the wait-count insertion loses track of
+    // loads issued under a branch and then waits for every outstanding load
+    // before each row. Rows past M re-read row M-1 and lanes past a short last
+    // chunk re-read its last pair; their results are dropped.
+    int64_t roff[RPW];
 #pragma unroll
-    for (int r = 0; r < QD_RMAX; ++r) acc[r] = 0.f;
+    for (int r = 0; r < RPW; ++r) roff[r] = (row0 + r < M ? row0 + r : M - 1) * nb1_w;
+
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.f;
 
     const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
-    uint32_t w[QD_RMAX][PW];
+    uint32_t w[RPW][PW];
     for (int64_t c = 0; c < nchunks; ++c) {
         const int64_t cb = nblk - c * QD_CH < QD_CH ? nblk - c * QD_CH : QD_CH;
-        const bool mine = nrows > 0 && 2 * lane < cb;  // this lane owns a pair of this chunk
-        const uint8_t* base = W + row0 * nb1_w + (c * QD_CH + 2 * lane) * BYTES;
+        const bool mine = 2 * lane < cb;  // this lane owns a pair of this chunk (cb is even)
+        const int pl = mine ? lane : (int) (cb / 2) - 1;
+        const uint8_t* base = W + (c * QD_CH + 2 * pl) * BYTES;
         auto issue = [&](int r) {
-            if (mine && r < nrows) {
-                const uint32_t* p32 = (const uint32_t*) (base + r * nb1_w);
+            const uint32_t* p32 = (const uint32_t*) (base + roff[r]);
 #pragma unroll
-                for (int i = 0; i < PW; ++i) w[r][i] = p32[i];
-            }
+            for (int i = 0; i < PW; ++i) w[r][i] = p32[i];
         };
         // x is loaded first (vector loads return in issue order), then the
         // weight stream starts so that it overlaps the conversion of x
         f4 xv[4];
         qd_load_x(x + c * QD_CH * QK, cb, xv);
 #pragma unroll
-        for (int r = 0; r < QD_PREFETCH; ++r) issue(r);
+        for (int r = 0; r < PF; ++r) issue(r);
+        // keep these loads above the prologue and its barrier
+        __builtin_amdgcn_sched_barrier(0);
         if (c > 0) __syncthreads();  // previous chunk's planes are no longer read
         qd_prologue(xv, cb, planes, scale_l, xsum_l);
         __syncthreads();
-        if (!mine) continue;
 
         // this lane's pair: planes of blocks A (groups 0-7) and B (groups 8-15)
         uint32_t PA[3][8], PB[3][8];
-        const uint32_t* src = planes + lane * QD_PSTRIDE;
+        const uint32_t* src = planes + pl * QD_PSTRIDE;
 #pragma unroll
         for (int p = 0; p < 3; ++p) {
 #pragma unroll
@@ -668,23 +678,34 @@ __global__ __launch_bounds__(256) void k_qmatvec_dot(const uint8_t* __restrict__
                 dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
             }
         }
-        const float sc[2] = {scale_l[2 * lane], scale_l[2 * lane + 1]};
-        const float xs[2] = {xsum_l[2 * lane], xsum_l[2 * lane + 1]};
+        const float sc[2] = {scale_l[2 * pl], scale_l[2 * pl + 1]};
+        const float xs[2] = {xsum_l[2 * pl], xsum_l[2 * pl + 1]};
 #pragma unroll
-        for (int r = 0; r < QD_RMAX; ++r) {
-            if (r + QD_PREFETCH < QD_RMAX) issue(r + QD_PREFETCH);
-            if (r < nrows) acc[r] += qd_pair<TYPE>(w[r], PA, PB, sc, xs);
+        for (int r = 0; r < RPW; ++r) {
+            if (r + PF < RPW) issue(r + PF);
+            __builtin_amdgcn_sched_barrier(0);  // row r + PF stays in flight during row r
+            const float v = qd_pair<TYPE>(w[r], PA, PB, sc, xs);
+            acc[r] += mine ? v : 0.f;
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
-    if (nrows == 0) return;
 #pragma unroll
-    for (int r = 0; r < QD_RMAX; ++r) acc[r] = wave_sum_lane63(acc[r]);
+    for (int r = 0; r < RPW; ++r) acc[r] = wave_sum_lane63(acc[r]);
     if (lane == 63) {
 #pragma unroll
-        for (int r = 0; r < QD_RMAX; ++r) {
-            if (r < nrows) y[row0 + r] = acc[r];
+        for (int r = 0; r < RPW; ++r) {
+            if (row0 + r < M) y[row0 + r] = acc[r];
         }
     }
+}
+
+template <int TYPE, int RPW>
+int launch_dot_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y, hipStream_t s) {
+    const int64_t waves = (M + RPW - 1) / RPW;
+    const int64_t grid = (waves + QD_WAVES - 1) / QD_WAVES;
+    hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s, (const uint8_t*) wq,
+                       nblk, M, (int64_t) nb1_w, x, y);
+    return check_launch("qmatvec_dot");
 }
 
 template <int TYPE>
@@ -695,11 +716,16 @@ int launch_qmatvec_dot(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, co
     int64_t rpw = (M + target_waves - 1) / target_waves;
     if (rpw > QD_RMAX) rpw = QD_RMAX;
     if (rpw < 1) rpw = 1;
-    const int64_t waves = (M + rpw - 1) / rpw;
-    const int64_t grid = (waves + 3) / 4;
-    hipLaunchKernelGGL((k_qmatvec_dot<TYPE>), dim3((unsigned) grid), dim3(256), 0, s, (const uint8_t*) wq, nblk, M,
-                       (int64_t) nb1_w, x, y, (int) rpw);
-    return check_launch("qmatvec_dot");
+    switch (rpw) {
+        case 1: return launch_dot_rpw<TYPE, 1>(wq, nblk, M, nb1_w, x, y, s);
+        case 2: return launch_dot_rpw<TYPE, 2>(wq, nblk, M, nb1_w, x, y, s);
+        case 3: return launch_dot_rpw<TYPE, 3>(wq, nblk, M, nb1_w, x, y, s);
+        case 4: return launch_dot_rpw<TYPE, 4>(wq, nblk, M, nb1_w, x, y, s);
+        case 5: return launch_dot_rpw<TYPE, 5>(wq, nblk, M, nb1_w, x, y, s);
+        case 6: return launch_dot_rpw<TYPE, 6>(wq, nblk, M, nb1_w, x, y, s);
+        case 7: return launch_dot_rpw<TYPE, 7>(wq, nblk, M, nb1_w, x, y, s);
+        default: return launch_dot_rpw<TYPE, 8>(wq, nblk, M, nb1_w, x, y, s);
+    }
 }
 
 int qv1_grid(int64_t M, int rows) {

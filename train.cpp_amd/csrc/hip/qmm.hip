@@ -57,7 +57,7 @@ constexpr uint32_t QM_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32
 // x in block fixed point, written by k_qmm_xprep and read by k_qmm on the
 // same stream. Planes: [block][digit][lane 0..63] 8 bytes each. Meta:
 // [block][field][column 0..15] with fields 2^-s (f32), sum of x (f32) and
-// sum of X (i32). Calls that overlap on one GPU race.
+// -bias * sum of X (i32; bias 8 for Q4_0, 16 for Q5_0, else 0). Calls that overlap on one GPU race.
 __device__ __attribute__((aligned(256))) uint64_t g_qm_planes[QM_MAX_BLOCKS * QM_PLANES * 64];
 __device__ __attribute__((aligned(256))) uint32_t g_qm_meta[QM_MAX_BLOCKS * 3 * 16];
 
@@ -71,70 +71,75 @@ __device__ __forceinline__ uint32_t pack_bytes(const int* v) {
            ((uint32_t) (v[3] & 0xFF) << 24);
 }
 
-// One wave per x block: lane (j, g) converts the 8 elements it feeds to the
-// MFMA for column j; lanes j, j+16, j+32, j+48 share the block maximum.
+// One thread per (block b, column j): it reads the block's 32 values, finds the
+// scale and writes the digit bytes of all four MFMA lanes j + 16g that carry
+// column j (no cross-lane traffic, so the kernel is one load and one store deep).
 __global__ __launch_bounds__(256) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk,
-                                                    int rot) {
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+                                                    int rot, int bias) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    const int b = t >> 4, j = t & 15;
     if (b >= nblk) return;
-    const int l = threadIdx.x & 63, j = l & 15, g = l >> 4;
-    const int c = (b & 1) ? 0 : rot;
-    const int e0 = (c + 4 * g) & 15, e1 = (c + 4 * g + 2) & 15;
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float v[32];
     if (j < N) {
-        const float* col = x + j * ldx + (int64_t) b * QK;
-        const float2 a0 = *(const float2*) (col + e0), a1 = *(const float2*) (col + e1);
-        const float2 h0 = *(const float2*) (col + 16 + e0), h1 = *(const float2*) (col + 16 + e1);
-        v[0] = a0.x; v[1] = a0.y; v[2] = a1.x; v[3] = a1.y;
-        v[4] = h0.x; v[5] = h0.y; v[6] = h1.x; v[7] = h1.y;
+        const f4* col = (const f4*) (x + j * ldx + (int64_t) b * QK);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const f4 w = col[q];
+            v[4 * q] = w.x; v[4 * q + 1] = w.y; v[4 * q + 2] = w.z; v[4 * q + 3] = w.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 32; ++e) v[e] = 0.f;
     }
     float mx = 0.f, sm = 0.f;
     int bad = 0;  // fmaxf drops NaN, so non-finite values are flagged separately
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        mx = fmaxf(mx, fabsf(v[i]));
-        sm += v[i];
-        bad |= !__builtin_isfinite(v[i]);
+    for (int e = 0; e < 32; ++e) {
+        mx = fmaxf(mx, fabsf(v[e]));
+        sm += v[e];
+        bad |= !__builtin_isfinite(v[e]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    sm += __shfl_xor(sm, 16, 64);
-    sm += __shfl_xor(sm, 32, 64);
-    bad |= __shfl_xor(bad, 16, 64);
-    bad |= __shfl_xor(bad, 32, 64);
     const bool finite = bad == 0;
     // mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^QM_XBITS
     const int s = (mx > 0.f && finite) ? QM_XBITS - __builtin_amdgcn_frexp_expf(mx) : 0;
-    int dg[QM_PLANES][8];
+    int dg[QM_PLANES][32];
     int sx = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int X = finite ? (int) __builtin_rintf(__builtin_ldexpf(v[i], s)) : 0;
+    for (int e = 0; e < 32; ++e) {
+        const int X = finite ? (int) __builtin_rintf(__builtin_ldexpf(v[e], s)) : 0;
         sx += X;
-        const int p0 = (int) (int8_t) (X & 0xFF);
-        const int X1 = (X - p0) >> 8;
-        dg[0][i] = p0;
+        // balanced base-256 digits: X = d0 + 256 d1 (+ 65536 d2), d0, d1 in [-128, 127]
+        const int X1 = (X + 128) >> 8;
+        dg[0][e] = X - (X1 << 8);
         if constexpr (QM_PLANES == 2) {
-            dg[1][i] = X1;  // |X1| <= 64
+            dg[1][e] = X1;  // |X1| <= 64
         } else {
-            const int p1 = (int) (int8_t) (X1 & 0xFF);
-            dg[1][i] = p1;
-            dg[2][i] = (X1 - p1) >> 8;  // |.| <= 32
+            const int X2 = (X1 + 128) >> 8;
+            dg[1][e] = X1 - (X2 << 8);
+            dg[2][e] = X2;  // |X2| <= 32
         }
     }
-    sx += __shfl_xor(sx, 16, 64);
-    sx += __shfl_xor(sx, 32, 64);
-    uint64_t* dst = g_qm_planes + (int64_t) b * QM_PLANES * 64 + l;
+    // lane group g feeds k = 8g..8g+7: elements E = (c + 4g + i) & 15 (i < 4), then 16 + E
+    const int c = (b & 1) ? 0 : rot;
+    uint64_t* dst = g_qm_planes + (int64_t) b * QM_PLANES * 64 + j;
 #pragma unroll
-    for (int p = 0; p < QM_PLANES; ++p) {
-        dst[64 * p] = (uint64_t) pack_bytes(dg[p]) | ((uint64_t) pack_bytes(dg[p] + 4) << 32);
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int p = 0; p < QM_PLANES; ++p) {
+            int lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // c is 0 or 2: select between two constant indices (no dynamic register indexing)
+                lo[i] = c ? dg[p][(2 + 4 * g + i) & 15] : dg[p][(4 * g + i) & 15];
+                hi[i] = c ? dg[p][16 + ((2 + 4 * g + i) & 15)] : dg[p][16 + ((4 * g + i) & 15)];
+            }
+            dst[64 * p + 16 * g] = (uint64_t) pack_bytes(lo) | ((uint64_t) pack_bytes(hi) << 32);
+        }
     }
-    if (g == 0) {
-        uint32_t* meta = g_qm_meta + b * 48 + j;
-        meta[0] = __builtin_bit_cast(uint32_t, finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf(""));
-        meta[16] = __builtin_bit_cast(uint32_t, sm);
-        meta[32] = (uint32_t) sx;
-    }
+    uint32_t* meta = g_qm_meta + b * 48 + j;
+    meta[0] = __builtin_bit_cast(uint32_t, finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf(""));
+    meta[16] = __builtin_bit_cast(uint32_t, sm);
+    meta[32] = (uint32_t) (-bias * sx);  // |.| <= 16 * 32 * 2^21 = 2^30
 }
 
 // Per format: which dwords of a pair each lane loads (NW of them), in bytes
@@ -193,8 +198,11 @@ __device__ __forceinline__ long nibbles(uint32_t w, uint32_t fifth) {
     uint32_t lo = w & 0x0F0F0F0Fu;
     uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
     if constexpr (FIVE) {
-        lo |= ((fifth & 0xFu) * 0x02040810u) & 0x10101010u;
-        hi |= (((fifth >> 4) & 0xFu) * 0x02040810u) & 0x10101010u;
+        // bit i of a 4-bit field -> bit 8i with one full-rate 24-bit multiply (a plain
+        // multiply would be folded with the shift into a quarter-rate 32-bit one),
+        // then to bit 4 of byte i
+        lo |= (__umul24(fifth & 0xFu, 0x00204081u) & 0x01010101u) << 4;
+        hi |= (__umul24((fifth >> 4) & 0xFu, 0x00204081u) & 0x01010101u) << 4;
     }
     return (long) ((uint64_t) lo | ((uint64_t) hi << 32));
 }
@@ -205,6 +213,16 @@ __device__ __forceinline__ uint32_t fifth_bits(uint32_t qh, int g) {
 }
 __device__ __forceinline__ uint32_t rot2_halves(uint32_t qh) {
     return ((qh >> 2) & 0x3FFF3FFFu) | ((qh << 14) & 0xC000C000u);
+}
+
+// Digit combination a0 + 256 a1 + 65536 a2 as two v_lshl_add_u32: the empty
+// asm keeps the compiler from folding it into two shifts and a three-way add.
+// (A real inline-asm v_lshl_add would read the MFMA results without the wait
+// states the compiler inserts for its own instructions.)
+__device__ __forceinline__ uint32_t combine3(int a0, int a1, int a2) {
+    uint32_t t = (uint32_t) a0 + ((uint32_t) a1 << 8);
+    asm("" : "+v"(t));
+    return t + ((uint32_t) a2 << 16);
 }
 
 struct QmBlocks {
@@ -254,7 +272,7 @@ constexpr int QM_RING = 3;     // chunks in flight: registers -> LDS ring depth
 struct QmX {
     long xp[2][QM_PLANES];
     f4 sc[2];
-    v4i aux[2];  // -BIAS * sum X (int) or the block sums of x (float bits)
+    v4i aux[2];  // -BIAS * sum X (int, the first MFMA's accumulator input) or the block sums of x (float bits)
 };
 
 template <int TYPE>
@@ -287,7 +305,7 @@ __device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32
     const v4i zero = {0, 0, 0, 0};
     v4i c0[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) c0[h] = BIAS != 0 ? x.aux[h] * (-BIAS) : zero;
+    for (int h = 0; h < 2; ++h) c0[h] = BIAS != 0 ? x.aux[h] : zero;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         uint32_t w[NW];
@@ -310,7 +328,7 @@ __device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32
                 } else if constexpr (QM_PLANES == 3) {
                     // modulo 2^32: the exact result fits in int32 (|q - bias| <= 31, |X| <= 2^21)
                     // even where the partial sums with the bias term would not
-                    qx = (float) (int) ((uint32_t) a0[i] + (uint32_t) a1[i] * 256u + (uint32_t) a2[i] * 65536u);
+                    qx = (float) (int) combine3(a0[i], a1[i], a2[i]);
                 } else {
                     qx = (float) (int) ((uint32_t) a0[i] + (uint32_t) a1[i] * 256u);
                 }
@@ -463,8 +481,9 @@ int launch_t(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t
 template <int TYPE>
 int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
                size_t nb1_y, hipStream_t s) {
-    hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) ((nblk + 3) / 4)), dim3(256), 0, s, x,
-                       (int64_t) (nb1_x / sizeof(float)), N, nblk, rotated_even<TYPE>() ? 2 : 0);
+    hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) ((nblk * 16 + 255) / 256)), dim3(256), 0, s, x,
+                       (int64_t) (nb1_x / sizeof(float)), N, nblk, rotated_even<TYPE>() ? 2 : 0,
+                       QmFmt<TYPE>::BIAS);
     const int rc = check_launch("qmm_xprep");
     if (rc != TRC_HIP_OK) return rc;
     // rows per workgroup: one workgroup per CU when M allows, 8-row granularity, at most 64
