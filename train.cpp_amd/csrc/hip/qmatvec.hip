@@ -469,7 +469,7 @@ constexpr int QD_WAVES = 8;       // waves per workgroup: one x conversion serve
 template <int TYPE>
 struct QdFmt {
     static constexpr int BYTES = block_bytes(TYPE);
-    static constexpr int PAIR_WORDS = 2 * BYTES / 4;  // 9, 10, 11, 12
+    static constexpr int PAIR_WORDS = 2 * BYTES / 4;  // 9, 10, 11, 12, 17
 };
 
 // x chunk -> byte planes in LDS. Thread t converts elements [16t, 16t+16) of
@@ -481,6 +481,12 @@ __device__ __forceinline__ void qd_load_x(const float* __restrict__ xc, int64_t 
     for (int i = 0; i < 4; ++i) v[i] = active ? ((const f4*) xc)[4 * t + i] : f4{0.f, 0.f, 0.f, 0.f};
 }
 
+// SIGNED: balanced digits X = D0 + 256 D1 + 65536 D2 with every D in [-128, 127]
+// (for the signed Q8_0 quants and v_dot4_i32_i8): the bytes of U = X + 0x808080
+// (0 < U < 2^24) are D + 128, so the planes of U with each byte's top bit
+// flipped are the digits. Otherwise P0, P1 are the unsigned low bytes of X and
+// P2 its signed top byte (for the unsigned nibble quants and v_dot4_u32_u8).
+template <bool SIGNED>
 __device__ __forceinline__ void qd_prologue(const f4* v, int64_t cb, uint32_t* planes, float* scale, float* xsum) {
     const int t = threadIdx.x;
     const int b = t >> 1, h = t & 1;
@@ -503,15 +509,20 @@ __device__ __forceinline__ void qd_prologue(const f4* v, int64_t cb, uint32_t* p
     uint32_t P[3][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t a = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].x, s));
-        const uint32_t bb = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].y, s));
-        const uint32_t c = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].z, s));
-        const uint32_t d = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].w, s));
+        constexpr uint32_t U = SIGNED ? 0x808080u : 0u;
+        const uint32_t a = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].x, s)) + U;
+        const uint32_t bb = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].y, s)) + U;
+        const uint32_t c = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].z, s)) + U;
+        const uint32_t d = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(v[i].w, s)) + U;
         const uint32_t t_ab = __builtin_amdgcn_perm(bb, a, 0x05010400u);  // a0 b0 a1 b1
         const uint32_t t_cd = __builtin_amdgcn_perm(d, c, 0x05010400u);   // c0 d0 c1 d1
         P[0][i] = __builtin_amdgcn_perm(t_cd, t_ab, 0x05040100u);         // a0 b0 c0 d0
         P[1][i] = __builtin_amdgcn_perm(t_cd, t_ab, 0x07060302u);         // a1 b1 c1 d1
         P[2][i] = __builtin_amdgcn_perm(bb, a, 0x0c0c0602u) | __builtin_amdgcn_perm(d, c, 0x06020c0cu);  // a2 b2 c2 d2
+        if constexpr (SIGNED) {
+#pragma unroll
+            for (int p = 0; p < 3; ++p) P[p][i] ^= 0x80808080u;
+        }
     }
     if (active) {
         // pair l = b>>1; within the pair, block (b&1) owns groups 8*(b&1) .. +7:
@@ -569,6 +580,26 @@ __device__ __forceinline__ float qd_block(const uint32_t* q, uint32_t qh, uint32
     return __builtin_fmaf(d, qx, half_bits_to_float(m_bits) * xs);
 }
 
+// One Q8_0 block of one row: 8 signed quant words against the balanced digit planes.
+__device__ __forceinline__ float qd_block_q8(const uint32_t* q, uint32_t d_bits, const uint32_t (*P)[8], float scale) {
+    int s0 = 0, s1 = 0, s2 = 0, t0 = 0, t1 = 0, t2 = 0;
+#pragma unroll
+    for (int w = 0; w < 8; w += 2) {
+        s0 = __builtin_amdgcn_sdot4((int) q[w], (int) P[0][w], s0, false);
+        s1 = __builtin_amdgcn_sdot4((int) q[w], (int) P[1][w], s1, false);
+        s2 = __builtin_amdgcn_sdot4((int) q[w], (int) P[2][w], s2, false);
+        t0 = __builtin_amdgcn_sdot4((int) q[w + 1], (int) P[0][w + 1], t0, false);
+        t1 = __builtin_amdgcn_sdot4((int) q[w + 1], (int) P[1][w + 1], t1, false);
+        t2 = __builtin_amdgcn_sdot4((int) q[w + 1], (int) P[2][w + 1], t2, false);
+    }
+    s0 += t0;
+    s1 += t1;
+    s2 += t2;
+    // sum_e q_e X_e = s0 + 256 s1 + 65536 s2; |s0 + 256 s1| < 2^27, s2 needs float
+    const float qx = __builtin_fmaf((float) s2, 65536.f, (float) (s0 + s1 * 256)) * scale;
+    return half_bits_to_float(d_bits) * qx;
+}
+
 // Decodes the dwords of a pair (pw, PAIR_WORDS of them) into the fields of its two blocks.
 template <int TYPE>
 __device__ __forceinline__ float qd_pair(const uint32_t* w, const uint32_t (*PA)[8], const uint32_t (*PB)[8],
@@ -589,11 +620,17 @@ __device__ __forceinline__ float qd_pair(const uint32_t* w, const uint32_t (*PA)
         for (int i = 0; i < 4; ++i) { qa[i] = align2(w[i + 2], w[i + 1]); qb[i] = w[7 + i]; }
         return qd_block<TYPE>(qa, align2(w[1], w[0]), w[0] & 0xFFFFu, 0, PA, sc[0], xs[0]) +
                qd_block<TYPE>(qb, w[6], w[5] >> 16, 0, PB, sc[1], xs[1]);
-    } else {  // Q5_1
+    } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) { qa[i] = w[2 + i]; qb[i] = w[8 + i]; }
         return qd_block<TYPE>(qa, w[1], w[0] & 0xFFFFu, w[0] >> 16, PA, sc[0], xs[0]) +
                qd_block<TYPE>(qb, w[7], w[6] & 0xFFFFu, w[6] >> 16, PB, sc[1], xs[1]);
+    } else {  // Q8_0: 17 dwords [d0 q0.0-1][q0 2-5] .. [q0 30-31 d1][q1 0-3] .. [q1 28-31]
+        uint32_t a8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a8[i] = align2(w[i + 1], w[i]);
+        (void) xs;
+        return qd_block_q8(a8, w[0] & 0xFFFFu, PA, sc[0]) + qd_block_q8(w + 9, w[8] >> 16, PB, sc[1]);
     }
 }
 
@@ -663,7 +700,7 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         // keep these loads above the prologue and its barrier
         __builtin_amdgcn_sched_barrier(0);
         if (c > 0) __syncthreads();  // previous chunk's planes are no longer read
-        qd_prologue(xv, cb, planes, scale_l, xsum_l);
+        qd_prologue<TYPE == TRC_HIP_TYPE_Q8_0>(xv, cb, planes, scale_l, xsum_l);
         __syncthreads();
 
         // this lane's pair: planes of blocks A (groups 0-7) and B (groups 8-15)
@@ -754,11 +791,9 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
     // 2 <= N <= 16: int8 matrix-core kernel (qmm.hip)
     if (qmm_supported(K, N, wq, nb1_w)) return launch_qmm(TYPE, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s);
     // N = 1 integer-dot kernel: pairs of blocks start on 4-byte boundaries
-    if constexpr (TYPE != TRC_HIP_TYPE_Q8_0) {
-        if (N == 1 && nblk % 2 == 0 && (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0 &&
-            (((uintptr_t) x) & 15u) == 0) {
-            return launch_qmatvec_dot<TYPE>(wq, nblk, M, nb1_w, x, y, s);
-        }
+    if (N == 1 && nblk % 2 == 0 && (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0 &&
+        (((uintptr_t) x) & 15u) == 0) {
+        return launch_qmatvec_dot<TYPE>(wq, nblk, M, nb1_w, x, y, s);
     }
     // N = 1 streaming kernel: needs 16-byte aligned rows and row chunks
     if (N == 1 && nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0) {
