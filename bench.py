@@ -334,7 +334,7 @@ def main():
     traffic = read_traffic()
     roofline = {"bound": "hbm", "achieved": head["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": head["GB/s"] / HBM_PEAK_GBS, "traffic": traffic,
-                "kernel": "k_qmatvec<Q4_0> (train.cpp_amd/csrc/hip/qmatvec.hip)",
+                "kernel": "k_qmatvec_dot<Q4_0> (train.cpp_amd/csrc/hip/qmatvec.hip)",
                 "algorithmic_bytes_per_launch": head["bytes"]}
 
     extra = {"device": f"{props.name.decode()} {props.arch.decode()} CUs={props.compute_units}"}

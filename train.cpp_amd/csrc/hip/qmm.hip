@@ -34,12 +34,15 @@
 // use c = 0 throughout. k_qmm_xprep writes the x digits in the same order, so
 // each lane loads its operand with one 8-byte load per digit plane.
 //
-// Work split: a workgroup owns up to 64 rows (T tiles of 16). Its QM_WAVES
-// waves split the K pairs evenly, and each wave streams its share of the
-// pairs of all T tiles with two pairs of loads in flight. The partial
-// sums are added across the waves through LDS in a fixed order, so results
-// are deterministic. Rows per workgroup are chosen so the grid covers every
-// CU once when M allows.
+// Work split: a workgroup (8 waves) owns up to 64 rows (T tiles of 16) and
+// walks K in chunks of 8 pairs. Each chunk is copied by the whole workgroup
+// with coalesced 16-byte buffer loads (loads landing in MFMA layout directly
+// would touch 16 rows per instruction and swamp the L1 with tag lookups),
+// three chunks ahead in registers, into a 3-buffer LDS ring; wave w computes
+// pair w of the chunk for all T tiles, so its x operands are loaded once per
+// chunk and reused over the tiles. The partial sums are added across the
+// waves through LDS in a fixed order, so results are deterministic. Rows per
+// workgroup are chosen so the grid covers every CU once when M allows.
 #include "common.h"
 
 namespace trc_hip {
