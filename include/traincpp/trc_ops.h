@@ -1,6 +1,7 @@
 // traincpp-compatible operator constructors used on the HIP backend's path
 // (subset of include/traincpp/trc_ops.h in the reference: views, cont, cast,
-// dup, mul_mat). They only build graph nodes; no computation happens here.
+// dup, mul_mat, and the add / acc / repeat_back nodes mul_mat's autograd
+// emits). They only build graph nodes; no computation happens here.
 #pragma once
 
 #include "trc_context.h"
@@ -31,5 +32,17 @@ Tensor* cast(Context* ctx, Tensor* a, Type type);
 // (i2, i3) uses a's plane (i2 % a2, i3 % a3). Extension: a may be a legacy
 // quant type (Q4_0/Q4_1/Q5_0/Q5_1/Q8_0) with b F32; the result is F32.
 Tensor* mul_mat(Context* ctx, Tensor* a, Tensor* b);
+
+// a + b with b broadcast to a's shape (each b dim equal to a's or 1); result has a's shape.
+Tensor* add(Context* ctx, Tensor* a, Tensor* b);
+
+// Sum of a over its repeats back to b's shape (a.ne[i] % b.ne[i] == 0).
+Tensor* repeat_back(Context* ctx, Tensor* a, Tensor* b);
+
+// a with b added into the region of a that starts `offset` bytes in and has
+// row/plane/batch strides nb1/nb2/nb3 (element stride = the type size). a and
+// b contiguous; inplace makes the result a full view of a. op_params hold
+// int32 {nb1, nb2, nb3, offset, inplace}.
+Tensor* acc(Context* ctx, Tensor* a, Tensor* b, size_t nb1, size_t nb2, size_t nb3, size_t offset, bool inplace);
 
 }  // namespace traincpp

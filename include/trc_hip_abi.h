@@ -161,6 +161,29 @@ int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w
  * compute_dup src/backends/cpu/trc_cpu_ops.cpp:219-236). Element size 1, 2, 4 or 8 B. */
 int trc_hip_cpy(const trc_hip_tensor* src, const trc_hip_tensor* dst, void* stream);
 
+/* ggml add, dst = a + b: dst has a's shape, b broadcasts (each b->ne[d] equals
+ * a->ne[d] or is 1); any 4-byte aligned strides. OP_ADD (src/ops/trc_ops.cpp:46,
+ * shape rule :19-32) as computed by compute_binary
+ * (src/backends/cpu/trc_cpu_ops.cpp:52-78): one rounding per element, so the
+ * result is bit-identical to the CPU's. F32 only. */
+int trc_hip_add_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst, void* stream);
+
+/* ggml acc: dst = a, then dst[offset + i0*4 + i1*nb1 + i2*nb2 + i3*nb3] += b[i]
+ * for every element of b. OP_ACC (src/core/trc_tensor.cpp:322-361, computed by
+ * compute_acc src/backends/cpu/trc_cpu_ops.cpp:954-999). a and dst contiguous
+ * F32 of one shape; with inplace != 0 the copy is skipped (dst is a's storage,
+ * as in the reference's inplace view). The region must lie inside a and must
+ * not overlap itself (TRC_HIP_E_SHAPE otherwise). Bit-identical to the CPU. */
+int trc_hip_acc_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst, size_t nb1,
+                    size_t nb2, size_t nb3, size_t offset, int inplace, void* stream);
+
+/* ggml repeat_back: dst (contiguous, every dst->ne[d] dividing a->ne[d]) = the
+ * sums of a over its repeats. OP_REPEAT_BACK (src/ops/trc_ops.cpp:458-470) as
+ * computed by compute_repeat_back (src/backends/cpu/trc_cpu_ops.cpp:932-952):
+ * each output is summed from 0 in a's linear element order, so the result is
+ * bit-identical to the CPU's. F32 only. */
+int trc_hip_repeat_back_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

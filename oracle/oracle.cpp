@@ -264,6 +264,102 @@ int orc_mul_mat(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
     return orc_mul_mat_cols(a, a_ne, a_nb, b, b_ne, b_nb, d, d_ne, d_nb, 0, b_ne[1], threads);
 }
 
+// ---------------------------------------------------------------- element-wise ops
+// Shared helpers: byte offset of linear element i of a strided tensor
+// (tensor_offset_linear, src/core/trc_tensor.cpp:94-102) and of the broadcast
+// source element for dst element i (offset_broadcast,
+// src/backends/cpu/trc_cpu_ops.cpp:18-28).
+static size_t lin_offset(const int64_t ne[4], const size_t nb[4], int64_t i) {
+    size_t off = 0;
+    for (int d = 0; d < 4; ++d) {
+        off += (size_t) (i % ne[d]) * nb[d];
+        i /= ne[d];
+    }
+    return off;
+}
+
+static size_t bcast_offset(const int64_t t_ne[4], const size_t t_nb[4], const int64_t shape_ne[4], int64_t i) {
+    size_t off = 0;
+    for (int d = 0; d < 4; ++d) {
+        const int64_t idx = i % shape_ne[d];
+        i /= shape_ne[d];
+        if (t_ne[d] != 1) off += (size_t) idx * t_nb[d];
+    }
+    return off;
+}
+
+static int64_t nelem(const int64_t ne[4]) { return ne[0] * ne[1] * ne[2] * ne[3]; }
+
+int orc_add(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
+            const void* b, const int64_t b_ne[4], const size_t b_nb[4],
+            void* d, const int64_t d_ne[4], const size_t d_nb[4]) {
+    for (int k = 0; k < 4; ++k) {
+        if (d_ne[k] != a_ne[k] || (b_ne[k] != a_ne[k] && b_ne[k] != 1)) return -1;
+    }
+    const uint8_t* pa = (const uint8_t*) a;
+    const uint8_t* pb = (const uint8_t*) b;
+    uint8_t* pd = (uint8_t*) d;
+    const int64_t n = nelem(d_ne);
+    for (int64_t i = 0; i < n; ++i) {
+        const float va = *(const float*) (pa + lin_offset(a_ne, a_nb, i));
+        const float vb = *(const float*) (pb + bcast_offset(b_ne, b_nb, d_ne, i));
+        *(float*) (pd + lin_offset(d_ne, d_nb, i)) = va + vb;
+    }
+    return 0;
+}
+
+int orc_acc(const void* a, const int64_t a_ne[4], const void* b, const int64_t b_ne[4], const size_t b_nb[4],
+            void* d, size_t nb1, size_t nb2, size_t nb3, size_t offset, int inplace) {
+    const size_t nbytes = (size_t) nelem(a_ne) * sizeof(float);
+    // region bound check of the acc constructor (src/core/trc_tensor.cpp:331-337)
+    size_t last = (size_t) (b_ne[0] - 1) * sizeof(float);
+    last += b_ne[1] > 1 ? (size_t) (b_ne[1] - 1) * nb1 : 0;
+    last += b_ne[2] > 1 ? (size_t) (b_ne[2] - 1) * nb2 : 0;
+    last += b_ne[3] > 1 ? (size_t) (b_ne[3] - 1) * nb3 : 0;
+    if (offset + last + sizeof(float) > nbytes) return -1;
+    if (!inplace) std::memcpy(d, a, nbytes);
+    const uint8_t* pb = (const uint8_t*) b;
+    uint8_t* pd = (uint8_t*) d;
+    const int64_t n = nelem(b_ne);
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t rem = i, idx[4];
+        for (int k = 0; k < 4; ++k) {
+            idx[k] = rem % b_ne[k];
+            rem /= b_ne[k];
+        }
+        const size_t od = offset + (size_t) idx[0] * sizeof(float) + (size_t) idx[1] * nb1 + (size_t) idx[2] * nb2 +
+                          (size_t) idx[3] * nb3;
+        float* t = (float*) (pd + od);
+        *t = *t + *(const float*) (pb + lin_offset(b_ne, b_nb, i));
+    }
+    return 0;
+}
+
+int orc_repeat_back(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const int64_t d_ne[4]) {
+    for (int k = 0; k < 4; ++k) {
+        if (d_ne[k] <= 0 || a_ne[k] % d_ne[k] != 0) return -1;
+    }
+    const size_t d_nb[4] = {sizeof(float), sizeof(float) * (size_t) d_ne[0],
+                            sizeof(float) * (size_t) (d_ne[0] * d_ne[1]),
+                            sizeof(float) * (size_t) (d_ne[0] * d_ne[1] * d_ne[2])};
+    std::memset(d, 0, (size_t) nelem(d_ne) * sizeof(float));
+    const uint8_t* pa = (const uint8_t*) a;
+    uint8_t* pd = (uint8_t*) d;
+    const int64_t n = nelem(a_ne);
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t rem = i;
+        size_t od = 0;
+        for (int k = 0; k < 4; ++k) {
+            const int64_t idx = rem % a_ne[k];
+            rem /= a_ne[k];
+            od += (size_t) (idx % d_ne[k]) * d_nb[k];
+        }
+        float* t = (float*) (pd + od);
+        *t = *t + *(const float*) (pa + lin_offset(a_ne, a_nb, i));
+    }
+    return 0;
+}
+
 // ---------------------------------------------------------------- rng
 // splitmix64 and its float draws: src/core/trc_rng.cpp:38-68.
 uint64_t orc_rng_next_u64(uint64_t* state) {

@@ -26,6 +26,16 @@
  *                        precision brute force with an fp32 error bound, and the
  *                        reference's compute_mul_mat through its CPU Device on
  *                        permuted views (oracle/_ref), compared bit for bit.
+ *   orc_add            - tests/test_ops.cpp:52-95 (same shape, broadcast), the
+ *                        PyTorch goldens tests/golden/add_same_* / add_bcast_*,
+ *                        numpy's float32 a + b with broadcasting, and the
+ *                        reference's compute_binary on strided views (oracle/_ref).
+ *   orc_acc            - tests/test_ops.cpp:1152-1220 (strided region, inplace 3D),
+ *                        a numpy slice-add on the same region, and the reference's
+ *                        compute_acc (oracle/_ref), bit for bit.
+ *   orc_repeat_back    - tests/test_ops.cpp:1128-1150, numpy's reshape-and-sum
+ *                        (float64 bound), and the reference's compute_repeat_back
+ *                        (oracle/_ref), bit for bit.
  */
 #pragma once
 
@@ -74,6 +84,27 @@ int orc_mul_mat_cols(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
                      const void* b, const int64_t b_ne[4], const size_t b_nb[4],
                      void* d, const int64_t d_ne[4], const size_t d_nb[4],
                      int64_t j_begin, int64_t j_end, int threads);
+
+/* ggml add, dst = a + b with b broadcast over dst's shape (dst has a's shape;
+ * every b dim equals dst's or is 1). Element order and the single rounding of
+ * a + b follow compute_binary (src/backends/cpu/trc_cpu_ops.cpp:52-78, with
+ * offset_broadcast :18-28); shape rule src/ops/trc_ops.cpp:19-32. Returns 0, or
+ * -1 on shapes add does not accept. */
+int orc_add(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
+            const void* b, const int64_t b_ne[4], const size_t b_nb[4],
+            void* d, const int64_t d_ne[4], const size_t d_nb[4]);
+/* ggml acc: d = a (skipped when inplace, then d must alias a) and, for every
+ * element i of b in linear order, d[offset + i0*4 + i1*nb1 + i2*nb2 + i3*nb3] +=
+ * b[i] (src/core/trc_tensor.cpp:322-361, compute_acc
+ * src/backends/cpu/trc_cpu_ops.cpp:954-999). a and d contiguous F32 of one
+ * shape. Returns 0, or -1 when the region leaves a. */
+int orc_acc(const void* a, const int64_t a_ne[4], const void* b, const int64_t b_ne[4], const size_t b_nb[4],
+            void* d, size_t nb1, size_t nb2, size_t nb3, size_t offset, int inplace);
+/* ggml repeat_back: d (contiguous, d_ne dividing a_ne) = sums of a over its
+ * repeats, each output accumulated from 0 in a's linear element order
+ * (src/ops/trc_ops.cpp:458-470, compute_repeat_back
+ * src/backends/cpu/trc_cpu_ops.cpp:932-952). Returns 0, or -1 on bad shapes. */
+int orc_repeat_back(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const int64_t d_ne[4]);
 
 /* splitmix64 stream (src/core/trc_rng.cpp:38-68). */
 uint64_t orc_rng_next_u64(uint64_t* state);

@@ -282,6 +282,89 @@ void test_linear_backward(Device* dev) {
     context_free(ctx);
 }
 
+// A Linear layer with bias whose weight is a view of a larger parameter and is
+// broadcast over the activations' planes, forward and backward, with the
+// backward nodes built exactly as the reference's autograd emits them for
+// parameters with gradient accumulators (src/core/trc_autograd.cpp):
+//   ADD   :220-227  dbias = repeat_back(G, bias)
+//   MULMAT:487-503  dW = repeat_back(transpose(mul_mat(transpose(G), transpose(x))), W), dx = mul_mat(transpose(W), G)
+//   VIEW  :191-195, :136-143 and :58-75  acc(P_acc, dW, W.nb1, W.nb2, W.nb3, W.view_offs, inplace)
+// The element-wise nodes are checked bit for bit against the oracle applied to
+// the device's own inputs to them; the products within the mul_mat bar.
+void test_autograd_linear_bias(Device* dev) {
+    std::printf("linear + bias autograd compositions (add / repeat_back / acc on the device)\n");
+    const int64_t K = 96, M = 80, T = 24, B2 = 4, A2 = 2, P2 = 3;
+    Context* ctx = context_new(1 << 20);
+    Tensor* P = new_tensor_4d(ctx, TYPE_F32, K, M, P2, 1);      // parameter holding W in planes 1..2
+    Tensor* Pacc = new_tensor_4d(ctx, TYPE_F32, K, M, P2, 1);   // its gradient accumulator
+    Tensor* bias = new_tensor_4d(ctx, TYPE_F32, M, 1, 1, 1);
+    Tensor* bacc = new_tensor_4d(ctx, TYPE_F32, M, 1, 1, 1);
+    Tensor* x = new_tensor_4d(ctx, TYPE_F32, K, T, B2, 1);
+    Tensor* G = new_tensor_4d(ctx, TYPE_F32, M, T, B2, 1);      // upstream gradient of y
+    Tensor* W = view_4d(ctx, P, K, M, A2, 1, (size_t) P->nb[2]);
+    Tensor* h = mul_mat(ctx, W, x);                             // [M, T, B2]
+    Tensor* y = add(ctx, h, bias);
+    Tensor* dbias = repeat_back(ctx, G, bias);
+    Tensor* bacc_node = acc(ctx, bacc, dbias, dbias->nb[1], dbias->nb[2], dbias->nb[3], 0, true);
+    Tensor* dAt = mul_mat(ctx, transpose(ctx, G), transpose(ctx, x));  // [K, M, B2] (transposed)
+    Tensor* dA = transpose(ctx, dAt);
+    Tensor* dW = repeat_back(ctx, dA, W);                      // reduce B2 planes onto W's A2
+    Tensor* pacc_node = acc(ctx, Pacc, dW, W->nb[1], W->nb[2], W->nb[3], (size_t) P->nb[2], true);
+    Tensor* dx = mul_mat(ctx, transpose(ctx, W), G);
+    Graph* g = graph_new(ctx);
+    for (Tensor* t : {y, bacc_node, pacc_node, dx}) graph_build_forward_expand(ctx, g, t);
+    EXPECT(graph_first_unsupported(g, dev) == nullptr);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    const std::vector<float> vP = normal((size_t) (K * M * P2), 21), vX = normal((size_t) (K * T * B2), 22),
+                             vG = normal((size_t) (M * T * B2), 23, 0.1f), vb = normal((size_t) M, 24),
+                             vPacc = normal((size_t) (K * M * P2), 25, 0.01f), vbacc = normal((size_t) M, 26, 0.01f);
+    tensor_set(P, vP.data(), 0, vP.size() * 4);
+    tensor_set(x, vX.data(), 0, vX.size() * 4);
+    tensor_set(G, vG.data(), 0, vG.size() * 4);
+    tensor_set(bias, vb.data(), 0, vb.size() * 4);
+    tensor_set(Pacc, vPacc.data(), 0, vPacc.size() * 4);
+    tensor_set(bacc, vbacc.data(), 0, vbacc.size() * 4);
+    EXPECT(dev->graph_compute(g));
+    auto get = [](const Tensor* t) {
+        std::vector<float> v((size_t) tensor_nelements(t));
+        tensor_get(t, v.data(), 0, v.size() * 4);
+        return v;
+    };
+    const std::vector<float> gh = get(h), gy = get(y), gdb = get(dbias), gdAt = get(dAt), gdW = get(dW),
+                             gPacc = get(Pacc), gbacc = get(bacc), gdx = get(dx);
+    auto same_bits = [](const std::vector<float>& u, const std::vector<float>& v) {
+        return u.size() == v.size() && std::memcmp(u.data(), v.data(), u.size() * 4) == 0;
+    };
+    // element-wise nodes: bitwise against the oracle on the device's own inputs
+    std::vector<float> wy(gy.size()), wdb((size_t) M), wdW((size_t) (K * M * A2));
+    EXPECT(orc_add(gh.data(), h->ne, h->nb, vb.data(), bias->ne, bias->nb, wy.data(), y->ne, y->nb) == 0);
+    EXPECT(orc_repeat_back(vG.data(), G->ne, G->nb, wdb.data(), dbias->ne) == 0);
+    EXPECT(orc_repeat_back(gdAt.data(), dA->ne, dA->nb, wdW.data(), dW->ne) == 0);
+    std::vector<float> wPacc = vPacc, wbacc = vbacc;
+    EXPECT(orc_acc(wbacc.data(), bacc->ne, gdb.data(), dbias->ne, dbias->nb, wbacc.data(), dbias->nb[1], dbias->nb[2],
+                   dbias->nb[3], 0, 1) == 0);
+    EXPECT(orc_acc(wPacc.data(), Pacc->ne, gdW.data(), dW->ne, dW->nb, wPacc.data(), W->nb[1], W->nb[2], W->nb[3],
+                   (size_t) P->nb[2], 1) == 0);
+    const bool ew_ok = same_bits(gy, wy) && same_bits(gdb, wdb) && same_bits(gdW, wdW) && same_bits(gbacc, wbacc) &&
+                       same_bits(gPacc, wPacc);
+    EXPECT(ew_ok);
+    bool plane0_kept = std::memcmp(gPacc.data(), vPacc.data(), (size_t) (K * M) * 4) == 0;  // outside the region
+    EXPECT(plane0_kept);
+    // products: the oracle on the host inputs, within the mul_mat bar
+    HostInputs in;
+    in.f32 = {{P, vP}, {x, vX}, {G, vG}};
+    const double eh = row_l2_error(gh, oracle_mul_mat(in, W, x), M);
+    const double edA = row_l2_error(gdAt, oracle_mul_mat(in, dAt->src[0], dAt->src[1]), K);
+    const double edx = row_l2_error(gdx, oracle_mul_mat(in, dx->src[0], dx->src[1]), K);
+    const bool mm_ok = eh <= 1e-4 && edA <= 1e-4 && edx <= 1e-4;
+    EXPECT(mm_ok);
+    std::printf("    [%s] add/repeat_back/acc bit-exact: %s; products err h %.2e dA %.2e dx %.2e\n",
+                (ew_ok && plane0_kept && mm_ok) ? " OK " : "FAIL", ew_ok ? "yes" : "NO", eh, edA, edx);
+    buffer_free(buf);
+    graph_free(g);
+    context_free(ctx);
+}
+
 // ---------------------------------------------------------------- GGUF
 
 void put(std::vector<uint8_t>& v, const void* p, size_t n) {
@@ -468,17 +551,21 @@ void test_fill_and_unsupported(Device* dev) {
     for (float v : vb) ok = ok && v == -3.0f;
     EXPECT(ok);
     // nodes the backend does not implement are reported, not run
-    Tensor* add_node = new_tensor_2d(ctx, TYPE_F32, 1000, 3);
-    add_node->op = OP_ADD;
-    add_node->src[0] = a;
-    add_node->src[1] = a;
-    add_node->nsrc = 2;
-    EXPECT(!dev->supports_op(add_node));
+    Tensor* mul_node = new_tensor_2d(ctx, TYPE_F32, 1000, 3);
+    mul_node->op = OP_MUL;
+    mul_node->src[0] = a;
+    mul_node->src[1] = a;
+    mul_node->nsrc = 2;
+    EXPECT(!dev->supports_op(mul_node));
+    EXPECT(dev->supports_op(add(ctx, a, a)));
+    Tensor* r2 = new_tensor_2d(ctx, TYPE_F32, 4, 2);
+    EXPECT(!dev->supports_op(acc(ctx, a, r2, 4, 0, 0, 0, false)));  // the region's rows overlap
+    EXPECT(dev->supports_op(acc(ctx, a, r2, 16, 0, 0, 0, false)));
     Tensor* hh = mul_mat(ctx, h, h);  // F16 mul_mat: not on this backend
     EXPECT(!dev->supports_op(hh));
     Graph* g = graph_new(ctx);
-    graph_build_forward_expand(ctx, g, add_node);
-    EXPECT(graph_first_unsupported(g, dev) == add_node);
+    graph_build_forward_expand(ctx, g, mul_node);
+    EXPECT(graph_first_unsupported(g, dev) == mul_node);
     std::printf("    [%s] fill + unsupported-op reporting\n", ok ? " OK " : "FAIL");
     buffer_free(buf);
     EXPECT(a->data == nullptr && a->buffer == nullptr);  // buffer_free detaches its tensors
@@ -508,6 +595,20 @@ void test_core_cpu(const std::string& dir) {
     EXPECT(graph_n_nodes(g) == 3 && graph_node(g, 2) == y && graph_n_leafs(g) == 2);
     EXPECT(std::string(op_name(OP_MUL_MAT)) == "mul_mat" && std::string(op_name(OP_WEIGHTNORM_SYNC)) == "weightnorm_sync");
     EXPECT(std::string(type_name(TYPE_Q5_1)) == "q5_1" && type_size(TYPE_Q8_0) == 34 && type_blck_size(TYPE_Q4_1) == 32);
+    // add / repeat_back / acc nodes (src/ops/trc_ops.cpp:46,458-470; src/core/trc_tensor.cpp:322-361)
+    Tensor* bb = new_tensor_4d(ctx, TYPE_F32, 6, 1, 4, 1);
+    Tensor* s = add(ctx, a, bb);
+    EXPECT(s->op == OP_ADD && s->src[1] == bb && s->ne[1] == 5 && s->ne[3] == 3);
+    Tensor* rb = repeat_back(ctx, a, bb);
+    EXPECT(rb->op == OP_REPEAT_BACK && rb->ne[0] == 6 && rb->ne[1] == 1 && rb->ne[2] == 4 && rb->ne[3] == 1);
+    Tensor* r2 = new_tensor_2d(ctx, TYPE_F32, 2, 2);
+    Tensor* ai = acc(ctx, a, r2, 24, 120, 480, 8, true);
+    int32_t prm[5];
+    std::memcpy(prm, ai->op_params, sizeof(prm));
+    EXPECT(ai->op == OP_ACC && ai->view_src == a && prm[0] == 24 && prm[1] == 120 && prm[2] == 480 && prm[3] == 8 &&
+           prm[4] == 1);
+    Tensor* an = acc(ctx, a, r2, 24, 120, 480, 8, false);
+    EXPECT(an->op == OP_ACC && an->view_src == nullptr && an->ne[2] == 4 && an->op_params[4] == 0);
     graph_free(g);
     context_free(ctx);
 
@@ -565,6 +666,7 @@ int main(int argc, char** argv) {
         test_registry(dev);
         test_conformance_mul_mat(dev);
         test_linear_backward(dev);
+        test_autograd_linear_bias(dev);
         test_gguf_config0(dev, dir);
         test_quantized_graph(dev, dir);
         test_fill_and_unsupported(dev);

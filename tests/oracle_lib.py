@@ -44,6 +44,12 @@ def oracle() -> C.CDLL:
         lib.orc_mul_mat.restype = I
         lib.orc_mul_mat_cols.argtypes = [P, NE, NB, P, NE, NB, P, NE, NB, I64, I64, I]
         lib.orc_mul_mat_cols.restype = I
+        lib.orc_add.argtypes = [P, NE, NB, P, NE, NB, P, NE, NB]
+        lib.orc_add.restype = I
+        lib.orc_acc.argtypes = [P, NE, P, NE, NB, P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, I]
+        lib.orc_acc.restype = I
+        lib.orc_repeat_back.argtypes = [P, NE, NB, P, NE]
+        lib.orc_repeat_back.restype = I
         lib.orc_rng_next_u64.argtypes = [C.POINTER(C.c_uint64)]
         lib.orc_rng_next_u64.restype = C.c_uint64
         lib.orc_rng_uniform01.argtypes = [C.POINTER(C.c_uint64)]
@@ -70,6 +76,12 @@ def ref() -> C.CDLL:
         lib.ref_dequant.restype = I
         lib.ref_mul_mat.argtypes = [P, NE, AX, P, NE, AX, P]
         lib.ref_mul_mat.restype = I
+        lib.ref_add.argtypes = [P, NE, AX, P, NE, AX, P]
+        lib.ref_add.restype = I
+        lib.ref_acc.argtypes = [P, NE, P, NE, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, I, P]
+        lib.ref_acc.restype = I
+        lib.ref_repeat_back.argtypes = [P, NE, AX, NE, P]
+        lib.ref_repeat_back.restype = I
         for n in ("ref_rng_next_u64", "ref_rng_uniform01"):
             getattr(lib, n).argtypes = [C.POINTER(C.c_uint64)]
         lib.ref_rng_next_u64.restype = C.c_uint64
@@ -150,6 +162,84 @@ def ref_mul_mat(a_base: np.ndarray, pa, b_base: np.ndarray, pb) -> np.ndarray:
     out = np.zeros((dne[3], dne[2], dne[1], dne[0]), dtype=np.float32)
     rc = ref().ref_mul_mat(a_base.ctypes.data, NE(*ane), AX(*pa), b_base.ctypes.data, NE(*bne), AX(*pb),
                            out.ctypes.data)
+    assert rc == 0, rc
+    return out
+
+
+def ggml_shape(ne) -> tuple:
+    """numpy shape (ne3, ne2, ne1, ne0) of a ggml ne."""
+    return (ne[3], ne[2], ne[1], ne[0])
+
+
+def add(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Oracle add of two (possibly strided) float32 views; result contiguous with a's shape."""
+    pa, ane, anb = base_ptr_and_meta(a)
+    pb, bne, bnb = base_ptr_and_meta(b)
+    out = np.zeros(ggml_shape(ane), dtype=np.float32)
+    _, dne, dnb = base_ptr_and_meta(out)
+    rc = oracle().orc_add(pa, NE(*ane), NB(*anb), pb, NE(*bne), NB(*bnb), out.ctypes.data, NE(*dne), NB(*dnb))
+    assert rc == 0, rc
+    return out
+
+
+def acc(a: np.ndarray, b: np.ndarray, nb1: int, nb2: int, nb3: int, offset: int, inplace: bool = False):
+    """Oracle acc: a contiguous (any rank up to 4), b a (possibly strided) view.
+    Returns the result array; when inplace, a itself is updated and returned."""
+    assert a.flags.c_contiguous and a.dtype == np.float32
+    _, ane, _ = base_ptr_and_meta(a)
+    pb, bne, bnb = base_ptr_and_meta(b)
+    out = a if inplace else np.empty_like(a)
+    rc = oracle().orc_acc(a.ctypes.data, NE(*ane), pb, NE(*bne), NB(*bnb), out.ctypes.data, nb1, nb2, nb3, offset,
+                          1 if inplace else 0)
+    assert rc == 0, rc
+    return out
+
+
+def repeat_back(a: np.ndarray, d_ne) -> np.ndarray:
+    """Oracle repeat_back of a (possibly strided) view onto ggml shape d_ne; contiguous result."""
+    pa, ane, anb = base_ptr_and_meta(a)
+    d_ne = list(d_ne) + [1] * (4 - len(d_ne))
+    out = np.zeros(ggml_shape(d_ne), dtype=np.float32)
+    rc = oracle().orc_repeat_back(pa, NE(*ane), NB(*anb), out.ctypes.data, NE(*d_ne))
+    assert rc == 0, rc
+    return out
+
+
+def _perm_ne(ne, axes):
+    # the reference's permute(): ne_out[i] = ne_in[axes[i]] (src/core/trc_tensor.cpp:303-306)
+    return [ne[axes[i]] for i in range(4)]
+
+
+def ref_add(a_base: np.ndarray, pa, b_base: np.ndarray, pb) -> np.ndarray:
+    """Reference library add(permute(A, pa), permute(B, pb)) on its CPU device."""
+    a_base = np.ascontiguousarray(a_base, dtype=np.float32)
+    b_base = np.ascontiguousarray(b_base, dtype=np.float32)
+    ane = list(a_base.shape)[::-1] + [1] * (4 - a_base.ndim)
+    bne = list(b_base.shape)[::-1] + [1] * (4 - b_base.ndim)
+    out = np.zeros(ggml_shape(_perm_ne(ane, pa)), dtype=np.float32)
+    rc = ref().ref_add(a_base.ctypes.data, NE(*ane), AX(*pa), b_base.ctypes.data, NE(*bne), AX(*pb), out.ctypes.data)
+    assert rc == 0, rc
+    return out
+
+
+def ref_acc(a: np.ndarray, b: np.ndarray, nb1: int, nb2: int, nb3: int, offset: int, inplace: bool) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    ane = list(a.shape)[::-1] + [1] * (4 - a.ndim)
+    bne = list(b.shape)[::-1] + [1] * (4 - b.ndim)
+    out = np.zeros_like(a)
+    rc = ref().ref_acc(a.ctypes.data, NE(*ane), b.ctypes.data, NE(*bne), nb1, nb2, nb3, offset, 1 if inplace else 0,
+                       out.ctypes.data)
+    assert rc == 0, rc
+    return out
+
+
+def ref_repeat_back(a_base: np.ndarray, pa, d_ne) -> np.ndarray:
+    a_base = np.ascontiguousarray(a_base, dtype=np.float32)
+    ane = list(a_base.shape)[::-1] + [1] * (4 - a_base.ndim)
+    d_ne = list(d_ne) + [1] * (4 - len(d_ne))
+    out = np.zeros(ggml_shape(d_ne), dtype=np.float32)
+    rc = ref().ref_repeat_back(a_base.ctypes.data, NE(*ane), AX(*pa), NE(*d_ne), out.ctypes.data)
     assert rc == 0, rc
     return out
 

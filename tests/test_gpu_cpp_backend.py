@@ -1,5 +1,6 @@
 """The HIP Device through the traincpp API on the GPU: conformance mul_mat
-graphs, linear-layer backward compositions, GGUF warm start (configuration 0)
+graphs, linear-layer backward compositions (with bias, broadcast weight planes
+and gradient accumulators: add / repeat_back / acc), GGUF warm start (configuration 0)
 and quantized tensors in graphs, each against the CPU oracle
 (tests/cpp/test_hip_backend.cpp)."""
 import os
@@ -22,3 +23,4 @@ def test_backend_through_traincpp_api(tmp_path):
     print(r.stderr)
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-2000:]
     assert "PASS: 0 failure(s)" in r.stdout
+    assert "add/repeat_back/acc bit-exact: yes" in r.stdout

@@ -1,0 +1,154 @@
+"""Parity of the element-wise graph ops the mul_mat autograd needs on the device
+(trc_hip_add_f32 / trc_hip_acc_f32 / trc_hip_repeat_back_f32) against the
+oracle's restatement of the reference CPU kernels (compute_binary, compute_acc,
+compute_repeat_back in src/backends/cpu/trc_cpu_ops.cpp).
+
+Bar (written here): bit-identical. Each output element is one IEEE add of the
+same two operands (add, acc) or the same ordered sum (repeat_back).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from conftest import announce
+from gpu_util import Dev, empty
+from traincpp_amd import hip as H
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(x):
+    return np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+
+
+def gpu_add(a_base, a_view, b_base, b_view):
+    da, db = Dev(a_base), Dev(b_base)
+    ne, _ = O.view_meta(a_view)
+    out = empty(O.ggml_shape(ne))
+    H.add_f32(da.tensor(a_view), db.tensor(b_view), out.tensor())
+    H.sync()
+    r = out.read()
+    for d in (da, db, out):
+        d.free()
+    return r
+
+
+@pytest.mark.parametrize("bshape", [(3, 5, 7, 33), (1, 5, 7, 33), (3, 1, 7, 1), (1, 1, 1, 33), (3, 5, 1, 1),
+                                    (1, 1, 1, 1)])
+def test_add_broadcast_bitwise(hip, bshape):
+    announce(f"add bcast {bshape}")
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((3, 5, 7, 33)).astype(np.float32)
+    b = rng.standard_normal(bshape).astype(np.float32)
+    got = gpu_add(a, a, b, b)
+    assert (bits(got) == bits(O.add(a, b))).all()
+
+
+def test_add_strided_views_bitwise(hip):
+    rng = np.random.default_rng(12)
+    A = rng.standard_normal((4, 6, 300, 9)).astype(np.float32)
+    B = rng.standard_normal((4, 6, 1, 9)).astype(np.float32)
+    av = A.transpose(0, 1, 3, 2)          # ggml [300, 9, 6, 4] with nb0 = 36 B
+    bv = B.transpose(0, 1, 3, 2)          # ggml [1, 9, 6, 4] with nb1 = 4 B: broadcast along ne0
+    got = gpu_add(A, av, B, bv)
+    assert (bits(got) == bits(O.add(av, bv))).all()
+
+
+def test_add_large_rows_bitwise(hip):
+    """Rows longer than a workgroup and more rows than the grid cap."""
+    rng = np.random.default_rng(13)
+    a = rng.standard_normal((2, 3000, 1037)).astype(np.float32)
+    b = rng.standard_normal((2, 1, 1037)).astype(np.float32)
+    got = gpu_add(a, a, b, b)
+    assert (bits(got) == bits(O.add(a, b))).all()
+
+
+def gpu_acc(t, b_base, b_view, nb1, nb2, nb3, off, inplace):
+    dt, db = Dev(t), Dev(b_base)
+    ta = dt.tensor()
+    if inplace:
+        H.acc_f32(ta, db.tensor(b_view), ta, nb1, nb2, nb3, off, True)
+        H.sync()
+        r = dt.read()
+        src = None
+    else:
+        out = empty(t.shape)
+        H.acc_f32(ta, db.tensor(b_view), out.tensor(), nb1, nb2, nb3, off, False)
+        H.sync()
+        r = out.read()
+        src = dt.read()
+        out.free()
+    dt.free()
+    db.free()
+    return r, src
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+def test_acc_regions_bitwise(hip, inplace):
+    announce(f"acc inplace={inplace}")
+    rng = np.random.default_rng(14)
+    t = rng.standard_normal((5, 40, 300)).astype(np.float32)   # ggml [300, 40, 5]
+    b = rng.standard_normal((3, 20, 250)).astype(np.float32)   # ggml [250, 20, 3]
+    nb1, nb2 = 300 * 4, 12000 * 4
+    off = (1 * 12000 + 7 * 300 + 11) * 4
+    got, src = gpu_acc(t, b, b, nb1, nb2, nb2 * 5, off, inplace)
+    want = O.acc(t.copy(), b, nb1, nb2, nb2 * 5, off, inplace=True)
+    assert (bits(got) == bits(want)).all()
+    if not inplace:
+        assert (bits(src) == bits(t)).all()  # the source target is left untouched
+    # a region that skips every other row, and the reference's own KAT shape
+    b2 = rng.standard_normal((20, 100)).astype(np.float32)
+    got, _ = gpu_acc(t, b2, b2, 2 * nb1, nb2, nb2, 4 * 3, inplace)
+    want = O.acc(t.copy(), b2, 2 * nb1, nb2, nb2, 12, inplace=True)
+    assert (bits(got) == bits(want)).all()
+    tk = np.arange(1, 9, dtype=np.float32).reshape(2, 4)
+    bk = np.array([[10, 20], [30, 40]], np.float32)
+    got, _ = gpu_acc(tk, bk, bk, 16, 0, 0, 4, inplace)
+    assert (got.reshape(-1) == [1, 12, 23, 4, 5, 36, 47, 8]).all()
+
+
+def test_acc_rejects_bad_regions(hip):
+    t = Dev(np.zeros((2, 4), np.float32))
+    b = Dev(np.ones((2, 2), np.float32))
+    with pytest.raises(H.HipError) as e:
+        H.acc_f32(t.tensor(), b.tensor(), t.tensor(), 16, 0, 0, 12, True)  # leaves the target
+    assert e.value.code == H.E_SHAPE
+    with pytest.raises(H.HipError) as e:
+        H.acc_f32(t.tensor(), b.tensor(), t.tensor(), 4, 0, 0, 0, True)  # rows overlap each other
+    assert e.value.code == H.E_SHAPE
+    t.free()
+    b.free()
+
+
+@pytest.mark.parametrize("d_ne", [[8, 5, 6, 4], [8, 1, 6, 4], [4, 5, 3, 2], [1, 1, 1, 1], [2, 5, 1, 4]])
+def test_repeat_back_bitwise(hip, d_ne):
+    announce(f"repeat_back {d_ne}")
+    rng = np.random.default_rng(15)
+    A = rng.standard_normal((4, 6, 5, 8)).astype(np.float32)  # ggml [8, 5, 6, 4]
+    for view in (A, A.transpose(0, 1, 3, 2)):
+        ne, _ = O.view_meta(view)
+        if any(ne[k] % d_ne[k] for k in range(4)):
+            continue
+        da = Dev(A)
+        out = empty(O.ggml_shape(d_ne))
+        H.repeat_back_f32(da.tensor(view), out.tensor())
+        H.sync()
+        got = out.read()
+        da.free()
+        out.free()
+        assert (bits(got) == bits(O.repeat_back(view, d_ne))).all()
+
+
+def test_repeat_back_mul_mat_broadcast_shape(hip):
+    """The shape mul_mat's backward reduces: dA of configuration 4
+    ([128, 1024, 32, 4] summed back to src0's [128, 1024, 8, 4])."""
+    rng = np.random.default_rng(16)
+    A = rng.standard_normal((4, 32, 1024, 128)).astype(np.float32)
+    da = Dev(A)
+    out = empty((4, 8, 1024, 128))
+    H.repeat_back_f32(da.tensor(), out.tensor())
+    H.sync()
+    got = out.read()
+    da.free()
+    out.free()
+    assert (bits(got) == bits(O.repeat_back(A, [128, 1024, 8, 4]))).all()

@@ -1,0 +1,179 @@
+"""Pins the oracle's add / acc / repeat_back (oracle/oracle.cpp) before the HIP
+kernels are compared against them:
+  - the reference's own known-answer tests (tests/test_ops.cpp:52-95, 1128-1220),
+  - its PyTorch goldens for add (tests/golden/add_same_*, add_bcast_*; tolerance
+    of tests/test_golden.cpp:190-201),
+  - numpy's float32 arithmetic where it performs the same single rounding
+    (add, acc) and a float64 bound where the summation order differs
+    (repeat_back),
+  - the reference library's own CPU kernels (oracle/_ref), bit for bit.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+GOLDEN = O.ROOT / "tests" / "golden"
+
+
+def _bits(x):
+    return np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------- known answers
+
+def test_add_kats():
+    # tests/test_ops.cpp:52-71 and :73-95
+    a = np.array([1, 2, 3, 4], np.float32)
+    b = np.array([10, 20, 30, 40], np.float32)
+    assert (O.add(a, b) == [11, 22, 33, 44]).all()
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)  # ggml [3, 2]
+    b = np.array([10, 20, 30], np.float32)             # ggml [3], broadcast along dim 1
+    assert (O.add(a, b) == np.array([[11, 22, 33], [14, 25, 36]], np.float32)).all()
+
+
+def test_repeat_back_kat():
+    # tests/test_ops.cpp:1128-1150: a [3,1] repeated to [3,4] then summed back = 4a
+    a = np.array([1, 2, 3], np.float32).reshape(1, 3)
+    rep = np.repeat(a, 4, axis=0)  # ggml [3, 4]
+    assert (O.repeat_back(rep, [3, 1]).reshape(-1) == [4, 8, 12]).all()
+
+
+def test_acc_kats():
+    # tests/test_ops.cpp:1152-1182: b [2,2] into target [4,2] at offset 4 B, nb1 = 16 B
+    t = np.arange(1, 9, dtype=np.float32).reshape(2, 4)
+    b = np.array([[10, 20], [30, 40]], np.float32)
+    r = O.acc(t, b, 16, 0, 0, 4)
+    assert (r.reshape(-1) == [1, 12, 23, 4, 5, 36, 47, 8]).all()
+    assert (t.reshape(-1) == np.arange(1, 9)).all()  # not inplace: target unchanged
+    # :1184-1220: inplace 3D, region at (i0=0, i1=1, i2=1) of a [2,3,4] target
+    t = np.arange(24, dtype=np.float32).reshape(4, 3, 2)
+    b = np.arange(100, 108, dtype=np.float32).reshape(2, 2, 2)
+    want = t.copy()
+    want[1:3, 1:3, 0:2] += b
+    O.acc(t, b, 8, 24, 96, 8 + 24, inplace=True)
+    assert (t == want).all()
+
+
+# ---------------------------------------------------------------- goldens
+
+@pytest.mark.parametrize("name", ["add_same", "add_bcast"])
+def test_add_goldens(name):
+    a = np.load(GOLDEN / f"{name}_in0.npy", allow_pickle=False).astype(np.float32)
+    b = np.load(GOLDEN / f"{name}_in1.npy", allow_pickle=False).astype(np.float32)
+    want = np.load(GOLDEN / f"{name}_out.npy", allow_pickle=False)
+    got = O.add(a, b)
+    assert np.allclose(got, want, atol=1e-4, rtol=1e-3)
+
+
+# ---------------------------------------------------------------- numpy closed forms
+
+def test_add_matches_numpy_broadcast_bitwise():
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((3, 5, 7, 9)).astype(np.float32)
+    for bshape in [(3, 5, 7, 9), (1, 5, 7, 9), (3, 1, 7, 1), (1, 1, 1, 9), (3, 5, 1, 1), (1, 1, 1, 1)]:
+        b = rng.standard_normal(bshape).astype(np.float32)
+        want = a + b  # numpy float32 add: one IEEE rounding per element, like the reference
+        assert (_bits(O.add(a, b)) == _bits(want)).all(), bshape
+    # strided (transposed) operands
+    at = a.transpose(0, 1, 3, 2)
+    b = rng.standard_normal((1, 5, 9, 1)).astype(np.float32)
+    assert (_bits(O.add(at, b)) == _bits(at + b)).all()
+
+
+def test_acc_matches_numpy_slice_add():
+    rng = np.random.default_rng(2)
+    t = rng.standard_normal((3, 6, 10)).astype(np.float32)  # ggml [10, 6, 3]
+    b = rng.standard_normal((2, 4, 5)).astype(np.float32)   # ggml [5, 4, 2]
+    nb1, nb2 = 10 * 4, 60 * 4
+    off = (1 * 60 + 2 * 10 + 3) * 4                          # start at (i0=3, i1=2, i2=1)
+    want = t.copy()
+    want[1:3, 2:6, 3:8] += b
+    assert (_bits(O.acc(t, b, nb1, nb2, nb2 * 3, off)) == _bits(want)).all()
+    # the region's row stride may skip rows: every other row of the target
+    b0 = np.ascontiguousarray(b[0, :3])  # ggml [5, 3] onto rows 0, 2, 4
+    want = t.copy()
+    want[0, 0:6:2, 0:5] += b0
+    assert (_bits(O.acc(t, b0, 2 * nb1, nb2, nb2, 0)) == _bits(want)).all()
+
+
+def test_acc_rejects_out_of_range_region():
+    t = np.zeros((2, 4), np.float32)
+    b = np.ones((2, 2), np.float32)
+    with pytest.raises(AssertionError):
+        O.acc(t, b, 16, 0, 0, 12)  # last element would land past the 8 floats
+
+
+def test_repeat_back_float64_bound():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((4, 6, 5, 8)).astype(np.float32)   # ggml [8, 5, 6, 4]
+    for d_ne in ([8, 5, 6, 4], [8, 1, 6, 4], [4, 5, 3, 2], [1, 1, 1, 1], [2, 5, 1, 4]):
+        got = O.repeat_back(a, d_ne)
+        r = [a.shape[3 - k] // d_ne[k] for k in range(4)]
+        t = a.astype(np.float64).reshape(r[3], d_ne[3], r[2], d_ne[2], r[1], d_ne[1], r[0], d_ne[0])
+        want = t.sum(axis=(0, 2, 4, 6))
+        nsum = int(np.prod(r))
+        bound = nsum * 2.0 ** -24 * np.abs(t).sum(axis=(0, 2, 4, 6)) + 1e-30
+        assert (np.abs(got - want) <= bound).all(), d_ne
+
+
+# ---------------------------------------------------------------- reference library
+
+pytestmark_ref = pytest.mark.skipif(not O.have_ref(), reason="oracle/_ref not built (reference checkout absent)")
+
+
+@pytestmark_ref
+@pytest.mark.parametrize("pa,pb,bshape", [
+    ((0, 1, 2, 3), (0, 1, 2, 3), None),
+    ((1, 0, 2, 3), (1, 0, 2, 3), None),
+    ((0, 2, 1, 3), (0, 1, 2, 3), (1,)),
+    ((1, 0, 2, 3), (0, 1, 2, 3), (2,)),
+])
+def test_add_bitwise_vs_reference(pa, pb, bshape):
+    rng = np.random.default_rng(4)
+    A = rng.standard_normal((3, 4, 5, 6)).astype(np.float32)   # base ggml [6, 5, 4, 3]
+    ane = [6, 5, 4, 3]
+    ape = [ane[pa[i]] for i in range(4)]
+    bne = [ape[O_pb] for O_pb in range(4)]
+    if bshape is not None:   # collapse some dims of b to 1 (broadcast)
+        for k in bshape:
+            bne[k] = 1
+    # b base laid out so that permute(b, pb) has shape bne
+    inv = [0] * 4
+    for i in range(4):
+        inv[pb[i]] = i
+    b_base_ne = [bne[inv[k]] for k in range(4)]
+    B = rng.standard_normal(tuple(b_base_ne[::-1])).astype(np.float32)
+    want = O.ref_add(A, pa, B, pb)
+    av = np.transpose(A, [3 - pa[3 - k] for k in range(4)])
+    bv = np.transpose(B, [3 - pb[3 - k] for k in range(4)])
+    got = O.add(av, bv)
+    assert (_bits(got) == _bits(want)).all()
+
+
+@pytestmark_ref
+@pytest.mark.parametrize("inplace", [False, True])
+def test_acc_bitwise_vs_reference(inplace):
+    rng = np.random.default_rng(5)
+    t = rng.standard_normal((4, 6, 10)).astype(np.float32)
+    b = rng.standard_normal((3, 4, 5)).astype(np.float32)
+    args = (10 * 4, 60 * 4, 240 * 4, (1 * 60 + 1 * 10 + 2) * 4)
+    want = O.ref_acc(t, b, *args, inplace)
+    got = O.acc(t.copy(), b, *args, inplace=inplace)
+    assert (_bits(got) == _bits(want)).all()
+
+
+@pytestmark_ref
+@pytest.mark.parametrize("pa,d_ne", [
+    ((0, 1, 2, 3), [8, 5, 6, 4]),
+    ((0, 1, 2, 3), [8, 1, 3, 1]),
+    ((1, 0, 2, 3), [5, 4, 2, 4]),
+    ((0, 2, 1, 3), [2, 6, 5, 2]),
+])
+def test_repeat_back_bitwise_vs_reference(pa, d_ne):
+    rng = np.random.default_rng(6)
+    A = rng.standard_normal((4, 6, 5, 8)).astype(np.float32)  # base ggml [8, 5, 6, 4]
+    want = O.ref_repeat_back(A, pa, d_ne)
+    av = np.transpose(A, [3 - pa[3 - k] for k in range(4)])
+    got = O.repeat_back(av, d_ne)
+    assert (_bits(got) == _bits(want)).all()

@@ -19,6 +19,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace traincpp {
@@ -48,6 +49,42 @@ size_t elem_size(Type t) {
         case TYPE_F64: case TYPE_I64: return 8;
         default: return 0;
     }
+}
+
+bool is_f32(const Tensor* t) { return t != nullptr && t->type == TYPE_F32; }
+
+// op_params of OP_ACC: int32 {nb1, nb2, nb3, offset, inplace} (src/core/trc_tensor.cpp:354-359).
+struct AccParams {
+    size_t nb1, nb2, nb3, offset;
+    bool inplace;
+};
+
+AccParams acc_params(const Tensor* t) {
+    int32_t p[5];
+    std::memcpy(p, t->op_params, sizeof(p));
+    return {(size_t) (uint32_t) p[0], (size_t) (uint32_t) p[1], (size_t) (uint32_t) p[2], (size_t) (uint32_t) p[3],
+            p[4] != 0};
+}
+
+// The acc region lies inside a and no two of its elements share an address
+// (the device adds every element of b concurrently).
+bool acc_region_ok(const Tensor* a, const Tensor* b, const AccParams& q) {
+    const size_t st[4] = {sizeof(float), q.nb1, q.nb2, q.nb3};
+    size_t last = 0;
+    for (int k = 0; k < 4; ++k) last += (size_t) (b->ne[k] - 1) * st[k];
+    if (q.offset + last + sizeof(float) > tensor_nbytes(a)) return false;
+    int idx[4] = {0, 1, 2, 3};
+    for (int i = 1; i < 4; ++i)
+        for (int j = i; j > 0 && st[idx[j]] < st[idx[j - 1]]; --j) std::swap(idx[j], idx[j - 1]);
+    size_t span = 0;
+    for (int i = 0; i < 4; ++i) {
+        const int k = idx[i];
+        if (b->ne[k] == 1) continue;
+        const size_t covered = span == 0 ? sizeof(float) : span;
+        if (st[k] < covered) return false;
+        span = st[k] * (size_t) (b->ne[k] - 1) + covered;
+    }
+    return true;
 }
 
 const Tensor* storage_root(const Tensor* t) {
@@ -170,6 +207,20 @@ public:
                 return legacy_quant(a->type) && a->nb[0] == type_size(a->type) && b->nb[0] == sizeof(float) &&
                        t->nb[0] == sizeof(float);
             }
+            case OP_ADD:  // compute_binary: b broadcasts where its extent is 1
+                return is_f32(a) && is_f32(b) && is_f32(t) && tensor_are_same_shape(a, t) && tensor_can_repeat(b, a);
+            case OP_ACC: {
+                if (!is_f32(a) || !is_f32(b) || !is_f32(t) || !tensor_are_same_shape(a, t)) return false;
+                if (!tensor_is_contiguous(a) || !tensor_is_contiguous(t)) return false;
+                return acc_region_ok(a, b, acc_params(t));
+            }
+            case OP_REPEAT_BACK: {
+                if (!is_f32(a) || !is_f32(t) || !tensor_is_contiguous(t)) return false;
+                for (int i = 0; i < 4; ++i) {
+                    if (a->ne[i] % t->ne[i] != 0) return false;
+                }
+                return true;
+            }
             default:
                 return false;
         }
@@ -264,6 +315,27 @@ private:
                     mul_mat_quant(t);
                 }
                 return;
+            case OP_ADD: {
+                const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
+                const trc_hip_tensor b = describe(t->src[1], need_buffer(t->src[1]));
+                const trc_hip_tensor d = describe(t, need_buffer(t));
+                check(trc_hip_add_f32(&a, &b, &d, nullptr), "add");
+                return;
+            }
+            case OP_ACC: {
+                const AccParams q = acc_params(t);
+                const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
+                const trc_hip_tensor b = describe(t->src[1], need_buffer(t->src[1]));
+                const trc_hip_tensor d = describe(t, need_buffer(t));
+                check(trc_hip_acc_f32(&a, &b, &d, q.nb1, q.nb2, q.nb3, q.offset, q.inplace ? 1 : 0, nullptr), "acc");
+                return;
+            }
+            case OP_REPEAT_BACK: {
+                const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
+                const trc_hip_tensor d = describe(t, need_buffer(t));
+                check(trc_hip_repeat_back_f32(&a, &d, nullptr), "repeat_back");
+                return;
+            }
             default:
                 unsupported(t);
         }

@@ -1,7 +1,11 @@
 // Operator constructors of the HIP path (graph nodes only). Shape rules follow
-// the reference's src/ops/trc_ops.cpp (cont :124-134, cast :136-147,
-// mul_mat :366-385) and src/core/trc_tensor.cpp (views :226-320).
+// the reference's src/ops/trc_ops.cpp (add :17-32/:46, cont :124-134,
+// cast :136-147, mul_mat :366-385, repeat_back :458-470) and
+// src/core/trc_tensor.cpp (views :226-320, acc :322-361).
 #include "impl.h"
+
+#include <climits>
+#include <cstring>
 
 namespace traincpp {
 
@@ -127,6 +131,57 @@ Tensor* mul_mat(Context* ctx, Tensor* a, Tensor* b) {
     r->src[0] = a;
     r->src[1] = b;
     r->nsrc = 2;
+    return r;
+}
+
+Tensor* add(Context* ctx, Tensor* a, Tensor* b) {
+    TRC_CHECK(a != nullptr && b != nullptr, "add: input is NULL");
+    TRC_CHECK(a->type == b->type, "add: input types differ (%s vs %s)", type_name(a->type), type_name(b->type));
+    TRC_CHECK(tensor_are_same_shape(a, b) || tensor_can_repeat(b, a), "add: b does not broadcast to a");
+    Tensor* r = new_tensor_nd(ctx, a->type, MAX_DIMS, a->ne);
+    r->op = OP_ADD;
+    r->src[0] = a;
+    r->src[1] = b;
+    r->nsrc = 2;
+    return r;
+}
+
+Tensor* repeat_back(Context* ctx, Tensor* a, Tensor* b) {
+    TRC_CHECK(a != nullptr && b != nullptr, "repeat_back: input is NULL");
+    for (int i = 0; i < MAX_DIMS; ++i) {
+        TRC_CHECK(a->ne[i] % b->ne[i] == 0, "repeat_back: a.ne[%d]=%lld is not a multiple of b.ne[%d]=%lld", i,
+                  (long long) a->ne[i], i, (long long) b->ne[i]);
+    }
+    Tensor* r = new_tensor_nd(ctx, a->type, MAX_DIMS, b->ne);
+    r->op = OP_REPEAT_BACK;
+    r->src[0] = a;
+    r->nsrc = 1;
+    return r;
+}
+
+Tensor* acc(Context* ctx, Tensor* a, Tensor* b, size_t nb1, size_t nb2, size_t nb3, size_t offset, bool inplace) {
+    TRC_CHECK(a != nullptr && b != nullptr, "acc: input is NULL");
+    TRC_CHECK(a->type == b->type, "acc: input types differ");
+    TRC_CHECK(tensor_is_contiguous(a), "acc: target must be contiguous");
+    TRC_CHECK(tensor_is_contiguous(b), "acc: source must be contiguous");
+    TRC_CHECK(type_is_supported(a->type), "acc: type %s is not supported", type_name(a->type));
+    const size_t nb0 = type_size(a->type);
+    size_t last = (size_t) (b->ne[0] - 1) * nb0;
+    last += b->ne[1] > 1 ? (size_t) (b->ne[1] - 1) * nb1 : 0;
+    last += b->ne[2] > 1 ? (size_t) (b->ne[2] - 1) * nb2 : 0;
+    last += b->ne[3] > 1 ? (size_t) (b->ne[3] - 1) * nb3 : 0;
+    TRC_CHECK(offset + last + nb0 <= tensor_nbytes(a), "acc: region out of range (offset=%zu last=%zu nbytes=%zu)",
+              offset, last, tensor_nbytes(a));
+    TRC_CHECK(nb1 <= (size_t) INT32_MAX && nb2 <= (size_t) INT32_MAX && nb3 <= (size_t) INT32_MAX &&
+                  offset <= (size_t) INT32_MAX,
+              "acc: strides and offset must fit int32");
+    Tensor* r = inplace ? make_view(ctx, a, OP_ACC, MAX_DIMS, a->ne, a->nb, 0) : tensor_dup_meta(ctx, a);
+    r->op = OP_ACC;
+    r->src[0] = a;
+    r->src[1] = b;
+    r->nsrc = 2;
+    const int32_t params[5] = {(int32_t) nb1, (int32_t) nb2, (int32_t) nb3, (int32_t) offset, inplace ? 1 : 0};
+    std::memcpy(r->op_params, params, sizeof(params));
     return r;
 }
 

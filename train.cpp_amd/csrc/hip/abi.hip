@@ -1,6 +1,6 @@
 // extern "C" entry points of libtrc_hip.so (declared in include/trc_hip_abi.h):
 // argument validation, error reporting and the HIP runtime calls. Kernels live
-// in dequant.hip, qmatvec.hip, mul_mat.hip and copy.hip.
+// in dequant.hip, qmatvec.hip, qmm.hip, mul_mat.hip, elementwise.hip and copy.hip.
 #include "common.h"
 
 #include <cstdarg>
@@ -261,6 +261,32 @@ int trc_hip_cpy(const trc_hip_tensor* src, const trc_hip_tensor* dst, void* stre
         return fail(TRC_HIP_E_ALIGN, "trc_hip_cpy: data not element aligned");
     }
     return launch_cpy(*src, *dst, es, (hipStream_t) stream);
+}
+
+int trc_hip_add_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst, void* stream) {
+    TRC_FORCED("trc_hip_add_f32");
+    if (a == nullptr || b == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_add_f32: NULL tensor");
+    if (a->data == nullptr || b->data == nullptr || dst->data == nullptr) {
+        return fail(TRC_HIP_E_INVALID, "trc_hip_add_f32: NULL data");
+    }
+    return launch_add_f32(*a, *b, *dst, (hipStream_t) stream);
+}
+
+int trc_hip_acc_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst, size_t nb1,
+                    size_t nb2, size_t nb3, size_t offset, int inplace, void* stream) {
+    TRC_FORCED("trc_hip_acc_f32");
+    if (a == nullptr || b == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_acc_f32: NULL tensor");
+    if (a->data == nullptr || b->data == nullptr || dst->data == nullptr) {
+        return fail(TRC_HIP_E_INVALID, "trc_hip_acc_f32: NULL data");
+    }
+    return launch_acc_f32(*a, *b, *dst, nb1, nb2, nb3, offset, inplace, (hipStream_t) stream);
+}
+
+int trc_hip_repeat_back_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream) {
+    TRC_FORCED("trc_hip_repeat_back_f32");
+    if (a == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_repeat_back_f32: NULL tensor");
+    if (a->data == nullptr || dst->data == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_repeat_back_f32: NULL data");
+    return launch_repeat_back_f32(*a, *dst, (hipStream_t) stream);
 }
 
 }  // extern "C"

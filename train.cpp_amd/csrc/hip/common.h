@@ -51,6 +51,10 @@ int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w,
 bool qmm_supported(int64_t K, int64_t N, const void* wq, size_t nb1_w);
 int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
                size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream);
+int launch_add_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t stream);
+int launch_acc_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, size_t nb1, size_t nb2,
+                   size_t nb3, size_t offset, int inplace, hipStream_t stream);
+int launch_repeat_back_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t stream);
 int launch_fill_f32(float* dst, float value, int64_t count, hipStream_t stream);
 int launch_cpy(const trc_hip_tensor& src, const trc_hip_tensor& dst, size_t elem_size,
                hipStream_t stream);

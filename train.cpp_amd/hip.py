@@ -23,6 +23,7 @@ EXPORTS = (
     "trc_hip_device_count", "trc_hip_init", "trc_hip_sync", "trc_hip_last_error",
     "trc_hip_malloc", "trc_hip_free", "trc_hip_h2d", "trc_hip_d2h", "trc_hip_memset",
     "trc_hip_fill_f32", "trc_hip_dequant", "trc_hip_mul_mat_f32", "trc_hip_qmatvec", "trc_hip_cpy",
+    "trc_hip_add_f32", "trc_hip_acc_f32", "trc_hip_repeat_back_f32",
 )
 
 
@@ -92,6 +93,9 @@ def load() -> C.CDLL:
         "trc_hip_mul_mat_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_qmatvec": ([I, P, I64, I64, SZ, P, I64, SZ, P, SZ, P], I),
         "trc_hip_cpy": ([C.POINTER(Tensor), C.POINTER(Tensor), P], I),
+        "trc_hip_add_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
+        "trc_hip_acc_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), SZ, SZ, SZ, SZ, I, P], I),
+        "trc_hip_repeat_back_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), P], I),
     }
     for name, (args, ret) in sig.items():
         fn = getattr(lib, name)
@@ -143,6 +147,20 @@ def qmatvec(type_: int, w_ptr: int, K: int, M: int, nb1_w: int, x_ptr: int, N: i
 
 def cpy(src: Tensor, dst: Tensor, stream: int | None = None) -> None:
     check(load().trc_hip_cpy(C.byref(src), C.byref(dst), stream))
+
+
+def add_f32(a: Tensor, b: Tensor, d: Tensor, stream: int | None = None) -> None:
+    check(load().trc_hip_add_f32(C.byref(a), C.byref(b), C.byref(d), stream))
+
+
+def acc_f32(a: Tensor, b: Tensor, d: Tensor, nb1: int, nb2: int, nb3: int, offset: int, inplace: bool,
+            stream: int | None = None) -> None:
+    check(load().trc_hip_acc_f32(C.byref(a), C.byref(b), C.byref(d), nb1, nb2, nb3, offset, 1 if inplace else 0,
+                                 stream))
+
+
+def repeat_back_f32(a: Tensor, d: Tensor, stream: int | None = None) -> None:
+    check(load().trc_hip_repeat_back_f32(C.byref(a), C.byref(d), stream))
 
 
 def fill_f32(ptr: int, value: float, count: int, stream: int | None = None) -> None:
