@@ -440,31 +440,34 @@ __global__ __launch_bounds__(QV1_WAVES * 64) void k_qmatvec_n1(const uint8_t* __
 //   - Each workgroup converts its chunk of x (4096 elements) once to block
 //     fixed point: per 32-element block b, X_e = rint(x_e * 2^s_b) with s_b
 //     chosen so |X_e| < 2^22, i.e. a 24-bit two's-complement integer with 22
-//     significant bits for the block maximum. The three bytes of every X_e are
-//     transposed into byte planes P0 (bits 0-7), P1 (8-15), P2 (16-23, signed)
-//     so that one dword of a plane holds 4 consecutive elements, the same
-//     element order as the quant bytes after the nibble split. Planes, 2^-s_b
-//     and the block sums of x go to LDS, then into each lane's registers.
-//   - Per row block, each quant word (8 elements) is split into low/high nibble
-//     bytes (3 ops) and multiplied against the planes with v_dot4_u32_u8 (P0,
-//     P1) and v_dot4_i32_i8 (P2): exact integer products and sums. The three
-//     plane sums are combined in float, scaled by 2^-s_b and by d; the bias
-//     (8 or 16) and the min (Q4_1/Q5_1) go through the block sum of x.
-//   - About 1.1 VALU ops per element instead of 2.4. The only rounding beyond
-//     FP32's is the 24-bit representation of x, whose error per element is at
-//     most 2^-23 of the block's largest |x|; the reference's own sequential
-//     FP32 sum of 32 products carries an error bound of the same order.
+//     significant bits for the block maximum. Planes, 2^-s_b and the block
+//     sums of x go to LDS, then into each lane's registers.
+//   - Q4_0 / Q4_1 (4-bit path): X is split into six balanced 4-bit digits, the
+//     digit planes are laid out in the quant words' own nibble order, and the
+//     quant words XOR 0x88888888 (signed q - 8) go straight into
+//     v_dot8_i32_i4: no nibble unpacking and no bias term, and the digit sums
+//     combine exactly in int32.
+//   - Q5_0 / Q5_1 / Q8_0 (byte path): the three bytes of every X_e are
+//     transposed into byte planes; Q5 quant words are split into nibble bytes
+//     with the fifth bit added (v_dot4_u32_u8 on the low planes,
+//     v_dot4_i32_i8 on the signed top plane); Q8_0 quants meet balanced signed
+//     byte digits of X with v_dot4_i32_i8. The plane sums are combined in
+//     float; the bias (16) and the min (Q5_1) go through the block sum of x.
+//   - The only rounding beyond FP32's is the 24-bit representation of x, whose
+//     error per element is at most 2^-23 of the block's largest |x|; the
+//     reference's own sequential FP32 sum of 32 products carries an error
+//     bound of the same order.
 //   - Each lane owns one pair of blocks of the chunk for every row its wave
-//     processes (pairs start on 4-byte boundaries for all formats); a wave
-//     handles a contiguous run of at most QD_RMAX rows with QD_PREFETCH rows of
-//     loads in flight; the per-row sums are reduced across the wave at the end.
+//     processes (pairs start on 4-byte boundaries for all formats). A wave
+//     handles at most QD_RMAX rows strided over all waves, with QD_PREFETCH
+//     rows of loads in flight; each row is reduced across the wave and stored
+//     as soon as its last chunk is done.
 
 constexpr int QD_CH = 128;        // blocks per chunk of K (one lane = one pair)
 constexpr int QD_RMAX = 8;        // rows per wave at most
 constexpr int QD_PREFETCH = 3;    // rows whose loads are in flight
 constexpr int QD_PSTRIDE = 52;    // LDS dwords per pair of planes (48 + 4: conflict-free b128 reads)
 constexpr int QD_WAVES = 8;       // waves per workgroup: one x conversion serves 8 waves
-                                  // (the first 256 threads convert, the rest wait at the barrier)
 
 template <int TYPE>
 struct QdFmt {
@@ -539,6 +542,97 @@ __device__ __forceinline__ void qd_prologue(const f4* v, int64_t cb, uint32_t* p
     }
 }
 
+// Bytes 0..2 of four 24-bit values, transposed: out[b] = byte b of (a, b_, c, d).
+__device__ __forceinline__ void bytes3_of4(uint32_t a, uint32_t b_, uint32_t c, uint32_t d, uint32_t* out) {
+    const uint32_t t_ab = __builtin_amdgcn_perm(b_, a, 0x05010400u);  // a0 b0 a1 b1
+    const uint32_t t_cd = __builtin_amdgcn_perm(d, c, 0x05010400u);   // c0 d0 c1 d1
+    out[0] = __builtin_amdgcn_perm(t_cd, t_ab, 0x05040100u);          // a0 b0 c0 d0
+    out[1] = __builtin_amdgcn_perm(t_cd, t_ab, 0x07060302u);          // a1 b1 c1 d1
+    out[2] = __builtin_amdgcn_perm(b_, a, 0x0c0c0602u) | __builtin_amdgcn_perm(d, c, 0x06020c0cu);  // a2 b2 c2 d2
+}
+
+// 4-bit path (Q4_0, Q4_1): X = D0 + 16 D1 + ... + 16^5 D5 with balanced digits
+// D in [-8, 7] (the nibbles of (X + 0x888888) ^ 0x888888), stored as six digit
+// planes whose words follow the quant words' own nibble order: quant byte j
+// holds element j (low nibble) and j + 16 (high nibble), so plane word g of a
+// block pairs element j with its low and j + 16 with its high nibble for the 4
+// bytes j of quant word g. Order B: word g = quant bytes 4g..4g+3. Order A (the
+// even block of a Q4_0 pair, whose quant bytes start 2 bytes into a dword):
+// word 0 = bytes 0, 1, 14, 15 and word g = bytes 4g-2..4g+1. The quant words,
+// XOR 0x88888888, become the signed nibbles q - 8, so v_dot8_i32_i4 gives
+// sum_e (q_e - 8) * X_e exactly in six digit sums.
+//
+// All QD_WAVES waves convert: thread t builds plane word g = t&3 of block t>>2
+// for the six planes from the 8 elements it needs (two pairs of low elements
+// and the same pairs + 16), loaded as float2; the block maximum, sum and
+// finiteness are reduced over the 4 threads of the block.
+struct QdX4 {
+    float2 v[4];  // low pair 0, low pair 1, high pair 0, high pair 1
+};
+static_assert(QD_WAVES * 64 == 4 * QD_CH, "four converting threads per block of a chunk");
+
+template <bool ORDER_A_EVEN>
+__device__ __forceinline__ void qd_load_x_n4(const float* __restrict__ xc, int64_t cb, QdX4& x) {
+    const int t = threadIdx.x;
+    const int b = t >> 2, g = t & 3;
+    const bool order_a = ORDER_A_EVEN && (b & 1) == 0;
+    const int j0 = order_a ? (g == 0 ? 0 : 4 * g - 2) : 4 * g;
+    const int j1 = order_a ? (g == 0 ? 14 : 4 * g) : 4 * g + 2;
+    const bool active = b < cb;
+    const float2* xb = (const float2*) (xc + 32 * (active ? b : 0));
+    const float2 z = {0.f, 0.f};
+    x.v[0] = active ? xb[j0 >> 1] : z;
+    x.v[1] = active ? xb[j1 >> 1] : z;
+    x.v[2] = active ? xb[(j0 + 16) >> 1] : z;
+    x.v[3] = active ? xb[(j1 + 16) >> 1] : z;
+}
+
+__device__ __forceinline__ void qd_prologue_n4(const QdX4& x, int64_t cb, uint32_t* planes, float* scale, float* xsum) {
+    const int t = threadIdx.x;
+    const int b = t >> 2, g = t & 3;
+    float mx = 0.f, sm = 0.f;
+    int bad = 0;  // fmaxf drops NaN, so non-finite values are flagged separately
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        mx = fmaxf(mx, fmaxf(fabsf(x.v[i].x), fabsf(x.v[i].y)));
+        sm += x.v[i].x + x.v[i].y;
+        bad |= !__builtin_isfinite(x.v[i].x) | !__builtin_isfinite(x.v[i].y);
+    }
+#pragma unroll
+    for (int m = 1; m <= 2; m <<= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+        sm += __shfl_xor(sm, m, 64);
+        bad |= __shfl_xor(bad, m, 64);
+    }
+    const bool finite = bad == 0;
+    // s = 22 - E with mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^22
+    const int s = (mx > 0.f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
+    uint32_t U[8];  // low elements 0-3, high elements 4-7
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int k = (i & 1) * 2 + (i >> 1) * 4;  // v[0] -> U0,1; v[1] -> U2,3; v[2] -> U4,5; v[3] -> U6,7
+        const uint32_t a0 = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(x.v[i].x, s));
+        const uint32_t a1 = (uint32_t) (int) __builtin_rintf(__builtin_ldexpf(x.v[i].y, s));
+        U[k] = (a0 + 0x888888u) ^ 0x888888u;
+        U[k + 1] = (a1 + 0x888888u) ^ 0x888888u;
+    }
+    if (b < cb) {
+        uint32_t BL[3], BH[3];
+        bytes3_of4(U[0], U[1], U[2], U[3], BL);
+        bytes3_of4(U[4], U[5], U[6], U[7], BH);
+        uint32_t* dst = planes + (b >> 1) * QD_PSTRIDE + 24 * (b & 1) + g;
+#pragma unroll
+        for (int y = 0; y < 3; ++y) {
+            dst[8 * y] = (BL[y] & 0x0F0F0F0Fu) | ((BH[y] & 0x0F0F0F0Fu) << 4);
+            dst[8 * y + 4] = ((BL[y] >> 4) & 0x0F0F0F0Fu) | (BH[y] & 0xF0F0F0F0u);
+        }
+        if (g == 0) {
+            scale[b] = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
+            xsum[b] = sm;
+        }
+    }
+}
+
 template <int TYPE>
 __device__ __forceinline__ void qd_unpack(uint32_t w, uint32_t qh_bits8, uint32_t& lo, uint32_t& hi) {
     lo = w & 0x0F0F0F0Fu;
@@ -580,6 +674,35 @@ __device__ __forceinline__ float qd_block(const uint32_t* q, uint32_t qh, uint32
     return __builtin_fmaf(d, qx, half_bits_to_float(m_bits) * xs);
 }
 
+// One Q4_0 / Q4_1 block of one row: 4 quant words (already XOR 0x88888888, i.e.
+// signed q - 8) against this lane's six 4-bit digit planes P[4*i + g]. Two
+// Horner chains (digits 5-4-3 and 2-1-0) carry the digit sums in their
+// accumulators, so only two start from zero; the result is exact in int32
+// (|sum| <= 32*8*2^22 = 2^30).
+template <int TYPE>
+__device__ __forceinline__ float qd_block_n4(const uint32_t* q, uint32_t d_bits, uint32_t m_bits, const uint32_t* P,
+                                             float scale, float xs) {
+    uint32_t hi = 0, lo = 0;
+#pragma unroll
+    for (int i = 2; i >= 0; --i) {
+        if (i < 2) {
+            hi <<= 4;
+            lo <<= 4;
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            hi = (uint32_t) __builtin_amdgcn_sdot8((int) q[g], (int) P[4 * (i + 3) + g], (int) hi, false);
+            lo = (uint32_t) __builtin_amdgcn_sdot8((int) q[g], (int) P[4 * i + g], (int) lo, false);
+        }
+    }
+    const int T = (int) ((hi << 12) + lo);
+    const float qx = (float) T * scale;  // sum_e (q_e - 8) x_e
+    const float d = half_bits_to_float(d_bits);
+    if constexpr (TYPE == TRC_HIP_TYPE_Q4_0) return d * qx;
+    // Q4_1: d * sum q x + m * sum x = d * (sum (q-8) x + 8 * sum x) + m * sum x
+    return __builtin_fmaf(d, __builtin_fmaf(8.f, xs, qx), half_bits_to_float(m_bits) * xs);
+}
+
 // One Q8_0 block of one row: 8 signed quant words against the balanced digit planes.
 __device__ __forceinline__ float qd_block_q8(const uint32_t* q, uint32_t d_bits, const uint32_t (*P)[8], float scale) {
     int s0 = 0, s1 = 0, s2 = 0, t0 = 0, t1 = 0, t2 = 0;
@@ -600,37 +723,52 @@ __device__ __forceinline__ float qd_block_q8(const uint32_t* q, uint32_t d_bits,
     return half_bits_to_float(d_bits) * qx;
 }
 
-// Decodes the dwords of a pair (pw, PAIR_WORDS of them) into the fields of its two blocks.
+// Whether a format runs on the 4-bit digit planes (v_dot8) or the byte planes (v_dot4).
 template <int TYPE>
-__device__ __forceinline__ float qd_pair(const uint32_t* w, const uint32_t (*PA)[8], const uint32_t (*PB)[8],
-                                         const float* sc, const float* xs) {
+constexpr bool qd_nibble_path() {
+    return TYPE == TRC_HIP_TYPE_Q4_0 || TYPE == TRC_HIP_TYPE_Q4_1;
+}
+
+// Decodes the dwords of a pair (PAIR_WORDS of them) into the fields of its two
+// blocks. PA / PB: this lane's 24 plane words of blocks A and B (six 4-bit
+// digit planes of 4 words, or three byte planes of 8 words).
+template <int TYPE>
+__device__ __forceinline__ float qd_pair(const uint32_t* w, const uint32_t* PA, const uint32_t* PB, const float* sc,
+                                         const float* xs) {
+    constexpr uint32_t FLIP = 0x88888888u;  // unsigned nibble q -> signed q - 8
+    const auto* PA3 = (const uint32_t(*)[8]) PA;
+    const auto* PB3 = (const uint32_t(*)[8]) PB;
     uint32_t qa[4], qb[4];
     if constexpr (TYPE == TRC_HIP_TYPE_Q4_0) {
+        // 36 B: [dA qA0-1][qA2-5][qA6-9][qA10-13][qA14-15 dB][qB0-3]..[qB12-15]
+        qa[0] = __builtin_amdgcn_perm(w[4], w[0], 0x05040302u) ^ FLIP;  // qA 0, 1, 14, 15
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { qa[i] = align2(w[i + 1], w[i]); qb[i] = w[5 + i]; }
-        return qd_block<TYPE>(qa, 0, w[0] & 0xFFFFu, 0, PA, sc[0], xs[0]) +
-               qd_block<TYPE>(qb, 0, w[4] >> 16, 0, PB, sc[1], xs[1]);
+        for (int i = 1; i < 4; ++i) qa[i] = w[i] ^ FLIP;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qb[i] = w[5 + i] ^ FLIP;
+        return qd_block_n4<TYPE>(qa, w[0] & 0xFFFFu, 0, PA, sc[0], xs[0]) +
+               qd_block_n4<TYPE>(qb, w[4] >> 16, 0, PB, sc[1], xs[1]);
     } else if constexpr (TYPE == TRC_HIP_TYPE_Q4_1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { qa[i] = w[1 + i]; qb[i] = w[6 + i]; }
-        return qd_block<TYPE>(qa, 0, w[0] & 0xFFFFu, w[0] >> 16, PA, sc[0], xs[0]) +
-               qd_block<TYPE>(qb, 0, w[5] & 0xFFFFu, w[5] >> 16, PB, sc[1], xs[1]);
+        for (int i = 0; i < 4; ++i) { qa[i] = w[1 + i] ^ FLIP; qb[i] = w[6 + i] ^ FLIP; }
+        return qd_block_n4<TYPE>(qa, w[0] & 0xFFFFu, w[0] >> 16, PA, sc[0], xs[0]) +
+               qd_block_n4<TYPE>(qb, w[5] & 0xFFFFu, w[5] >> 16, PB, sc[1], xs[1]);
     } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) { qa[i] = align2(w[i + 2], w[i + 1]); qb[i] = w[7 + i]; }
-        return qd_block<TYPE>(qa, align2(w[1], w[0]), w[0] & 0xFFFFu, 0, PA, sc[0], xs[0]) +
-               qd_block<TYPE>(qb, w[6], w[5] >> 16, 0, PB, sc[1], xs[1]);
+        return qd_block<TYPE>(qa, align2(w[1], w[0]), w[0] & 0xFFFFu, 0, PA3, sc[0], xs[0]) +
+               qd_block<TYPE>(qb, w[6], w[5] >> 16, 0, PB3, sc[1], xs[1]);
     } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) { qa[i] = w[2 + i]; qb[i] = w[8 + i]; }
-        return qd_block<TYPE>(qa, w[1], w[0] & 0xFFFFu, w[0] >> 16, PA, sc[0], xs[0]) +
-               qd_block<TYPE>(qb, w[7], w[6] & 0xFFFFu, w[6] >> 16, PB, sc[1], xs[1]);
+        return qd_block<TYPE>(qa, w[1], w[0] & 0xFFFFu, w[0] >> 16, PA3, sc[0], xs[0]) +
+               qd_block<TYPE>(qb, w[7], w[6] & 0xFFFFu, w[6] >> 16, PB3, sc[1], xs[1]);
     } else {  // Q8_0: 17 dwords [d0 q0.0-1][q0 2-5] .. [q0 30-31 d1][q1 0-3] .. [q1 28-31]
         uint32_t a8[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) a8[i] = align2(w[i + 1], w[i]);
         (void) xs;
-        return qd_block_q8(a8, w[0] & 0xFFFFu, PA, sc[0]) + qd_block_q8(w + 9, w[8] >> 16, PB, sc[1]);
+        return qd_block_q8(a8, w[0] & 0xFFFFu, PA3, sc[0]) + qd_block_q8(w + 9, w[8] >> 16, PB3, sc[1]);
     }
 }
 
@@ -665,7 +803,10 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
 
     const int lane = threadIdx.x & 63;
     const int64_t wave_id = (int64_t) blockIdx.x * QD_WAVES + (threadIdx.x >> 6);
-    const int64_t row0 = wave_id * RPW;
+    // Rows are strided over the waves (row = wave + r * n_waves), so the loads
+    // in flight at any time sweep W in address order rather than starting in
+    // every wave's own region.
+    const int64_t n_waves = (int64_t) gridDim.x * QD_WAVES;
 
     // No branches around loads and uses: the wait-count insertion loses track of
     // loads issued under a branch and then waits for every outstanding load
@@ -673,7 +814,10 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
     // chunk re-read its last pair; their results are dropped.
     int64_t roff[RPW];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) roff[r] = (row0 + r < M ? row0 + r : M - 1) * nb1_w;
+    for (int r = 0; r < RPW; ++r) {
+        const int64_t row = wave_id + r * n_waves;
+        roff[r] = (row < M ? row : M - 1) * nb1_w;
+    }
 
     float acc[RPW];
 #pragma unroll
@@ -694,26 +838,40 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         // x is loaded first (vector loads return in issue order), then the
         // weight stream starts so that it overlaps the conversion of x
         f4 xv[4];
-        qd_load_x(x + c * QD_CH * QK, cb, xv);
+        QdX4 xn;
+        if constexpr (qd_nibble_path<TYPE>()) {
+            qd_load_x_n4<TYPE == TRC_HIP_TYPE_Q4_0>(x + c * QD_CH * QK, cb, xn);
+        } else {
+            qd_load_x(x + c * QD_CH * QK, cb, xv);
+        }
 #pragma unroll
         for (int r = 0; r < PF; ++r) issue(r);
         // keep these loads above the prologue and its barrier
         __builtin_amdgcn_sched_barrier(0);
         if (c > 0) __syncthreads();  // previous chunk's planes are no longer read
-        qd_prologue<TYPE == TRC_HIP_TYPE_Q8_0>(xv, cb, planes, scale_l, xsum_l);
+        if constexpr (qd_nibble_path<TYPE>()) {
+            qd_prologue_n4(xn, cb, planes, scale_l, xsum_l);
+        } else {
+            qd_prologue<TYPE == TRC_HIP_TYPE_Q8_0>(xv, cb, planes, scale_l, xsum_l);
+        }
         __syncthreads();
 
-        // this lane's pair: planes of blocks A (groups 0-7) and B (groups 8-15)
-        uint32_t PA[3][8], PB[3][8];
+        // this lane's pair: the plane words of blocks A and B (24 each). Nibble
+        // path: A at dwords 0-23, B at 24-47. Byte path: plane p of A at
+        // 16p..16p+7 and of B at 16p+8..16p+15.
+        uint32_t PA[24], PB[24];
         const uint32_t* src = planes + pl * QD_PSTRIDE;
 #pragma unroll
-        for (int p = 0; p < 3; ++p) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const uint4 v = *(const uint4*) (src + 16 * p + 4 * g);
-                uint32_t* dst = g < 2 ? &PA[p][4 * g] : &PB[p][4 * (g - 2)];
-                dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+        for (int k = 0; k < 12; ++k) {
+            const uint4 v = *(const uint4*) (src + 4 * k);
+            uint32_t* dst;
+            if constexpr (qd_nibble_path<TYPE>()) {
+                dst = k < 6 ? &PA[4 * k] : &PB[4 * (k - 6)];
+            } else {
+                const int p = k >> 2, g = k & 3;
+                dst = g < 2 ? &PA[8 * p + 4 * g] : &PB[8 * p + 4 * (g - 2)];
             }
+            dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
         }
         const float sc[2] = {scale_l[2 * pl], scale_l[2 * pl + 1]};
         const float xs[2] = {xsum_l[2 * pl], xsum_l[2 * pl + 1]};
@@ -723,15 +881,15 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
             __builtin_amdgcn_sched_barrier(0);  // row r + PF stays in flight during row r
             const float v = qd_pair<TYPE>(w[r], PA, PB, sc, xs);
             acc[r] += mine ? v : 0.f;
+            // after the last chunk a row is final: reduce and store it while the
+            // next rows' loads are in flight, so the wave ends one reduction
+            // after its last row instead of RPW
+            if (c == nchunks - 1) {
+                const float sum = wave_sum_lane63(acc[r]);
+                const int64_t row = wave_id + r * n_waves;
+                if (lane == 63 && row < M) y[row] = sum;
+            }
             __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = wave_sum_lane63(acc[r]);
-    if (lane == 63) {
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            if (row0 + r < M) y[row0 + r] = acc[r];
         }
     }
 }
