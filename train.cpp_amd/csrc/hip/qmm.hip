@@ -1,38 +1,41 @@
-// H2 for 2 <= N <= 16 columns: fused dequant x skinny GEMM on the int8 matrix
-// cores (v_mfma_i32_16x16x32_i8).
+// H2 for 2 <= N <= 16 columns: fused dequant x skinny GEMM on the fp16 matrix
+// cores (v_mfma_f32_16x16x32_f16).
 //
 // Result to reproduce: gguf_tensor_to_f32 (src/io/trc_gguf.cpp:966-1049,
 // dequantize_q* :320-417) followed by compute_mul_mat
 // (src/backends/cpu/trc_cpu_ops.cpp:182-216); parity is by tolerance.
 //
 // Numerics. Within one 32-element block b of one row m
-//   sum_e (q_e*d + mn) * x_e,j = d * sum_e q_e * x_e,j + mn * sum_e x_e,j.
-// x is converted once per call (k_qmm_xprep) to block fixed point: for every
-// block b and column j, X_e = rint(x_e * 2^s) with s chosen so |X_e| <= 2^21,
-// i.e. 22 significant bits for the block's largest |x|. X is split into three
-// signed byte digits, X = P0 + 256 P1 + 65536 P2 (P0, P1 in [-128, 127],
-// |P2| <= 32). The quants enter the MFMAs unsigned (0..31) or as int8 (Q8_0);
-// the Q4_0/Q5_0 bias goes into the first MFMA's accumulator input as
-// -bias * sum_e X_e. The three MFMAs per block then give exact integer sums
-// that combine into one int32 for Q4_0/Q4_1/Q5_0/Q5_1 (the exact result is
-// below 2^31 since |q - bias| <= 31), and in float for Q8_0. One conversion
-// and two float operations apply 2^-s and d. The only rounding beyond FP32's is
-// the 22-bit representation of x (at most 2^-22 of the block maximum per
-// element), the same order as the reference's own FP32 sum over 32 products.
-// A block of x holding Inf or NaN turns its columns' outputs into NaN.
+//   sum_e (q_e*d + mn) * x_e,j = d * sum_e (q_e - bias) * x_e,j + mn * sum_e x_e,j.
+// The integer quants q_e - bias (|.| <= 128) are exact in fp16. x is converted
+// once per call (k_qmm_xprep): every column j is scaled by a power of two 2^s_j
+// so that max|x'| < 2^14, and x' = x * 2^s_j is split into two fp16 planes,
+// hi = fp16(x') and lo = fp16(x' - hi), about 22 significant bits. Both planes
+// go through the MFMA into one fp32 accumulator (every product of an 11-bit
+// and a 9-bit integer is exact), so a block needs one fused multiply-add by d
+// per output; 2^-s_j is applied once at the end. Elements more than 2^28 below
+// their column's largest |x| fall below fp16's range and drop out; their share
+// of the column's outputs is below FP32's own rounding. A column holding Inf
+// or NaN comes out NaN.
+//
+// Quants to fp16 without a conversion instruction: a nibble n OR'ed into the
+// mantissa of 1024.0 (0x6400) is the fp16 value 1024 + n, and at bits 4-7 it
+// is 1024 + 16n; one packed fp16 add (or fma by 1/16) then gives n - bias
+// exactly. Q8_0 bytes go the same way after their sign bits are flipped.
 //
 // Operand layout (lane l, m16 = l % 16, g = l / 16):
-//   A (16 x 32, i8)  = x digits: row = column j = m16 of x, k = 8g .. 8g+7
-//   B (32 x 16, i8)  = quants:   column = row m16 of the W tile, k = 8g .. 8g+7
-//   D (16 x 16, i32) = lane holds rows 4g .. 4g+3 (columns j of y), column m16.
-// k -> element order. Lane g's 8 k values are 4 low-nibble elements
-// E(g, i) = (c + 4g + i) & 15, i = 0..3, and the 4 high-nibble elements
-// 16 + E(g, i). For Q4_0, Q5_0 and Q8_0, blocks come in pairs whose second
-// block starts on a 4-byte boundary: odd blocks use c = 0 and even blocks c = 2.
-// With c = 2 the quant bytes a lane needs are one aligned dword, or
-// (lane group 3) one v_perm of two. Q4_1/Q5_1 blocks are 4-byte aligned and
-// use c = 0 throughout. k_qmm_xprep writes the x digits in the same order, so
-// each lane loads its operand with one 8-byte load per digit plane.
+//   A (16 x 32, f16) = x planes: row = column j = m16 of x, k = 8g .. 8g+7
+//   B (32 x 16, f16) = quants:   column = row m16 of the W tile, k = 8g .. 8g+7
+//   D (16 x 16, f32) = lane holds rows 4g .. 4g+3 (columns j of y), column m16.
+// k -> element order. Lane group g's quant bytes hold the elements
+// e_p = (c + 4g + p) & 15 (low nibble or Q8_0 low dword) and e_p + 16, p = 0..3,
+// and its 8 k values are, in order, e0, e2, e0+16, e2+16, e1, e3, e1+16, e3+16.
+// For Q4_0, Q5_0 and Q8_0, blocks come in pairs whose second block starts on a
+// 4-byte boundary: odd blocks use c = 0 and even blocks c = 2, so the quant
+// bytes a lane needs are one aligned dword or (lane group 3) one v_perm of two.
+// Q4_1/Q5_1 blocks are 4-byte aligned and use c = 0 throughout. k_qmm_xprep
+// writes the x planes in the same order, so each lane loads its A operand of a
+// block with one 16-byte load per plane.
 //
 // Work split: a workgroup (8 waves) owns up to 64 rows (T tiles of 16) and
 // walks K in chunks of 8 pairs. Each chunk is copied by the whole workgroup
@@ -48,101 +51,80 @@
 namespace trc_hip {
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int QM_MAX_BLOCKS = 2048;  // K <= 65536
 constexpr int QM_WAVES = 8;
-constexpr int QM_PLANES = 3;          // byte digits of x per element (2 would give 15-bit x: too coarse
-                                      // for the 1e-4 bar on short rows)
-constexpr int QM_XBITS = QM_PLANES == 3 ? 21 : 14;  // |X| <= 2^QM_XBITS
+constexpr int QM_CHB = 16;            // blocks per K chunk (8 pairs, one per wave)
+constexpr int QM_XBITS = 14;          // max|x'| < 2^14 keeps hi and its rounding inside fp16
+constexpr int QM_META_XS = QM_MAX_BLOCKS / QM_CHB * 16;  // block sums follow the chunk scales
 constexpr uint32_t QM_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
 
-// x in block fixed point, written by k_qmm_xprep and read by k_qmm on the
-// same stream. Planes: [block][digit][lane 0..63] 8 bytes each. Meta:
-// [block][field][column 0..15] with fields 2^-s (f32), sum of x (f32) and
-// -bias * sum of X (i32; bias 8 for Q4_0, 16 for Q5_0, else 0). Calls that overlap on one GPU race.
-__device__ __attribute__((aligned(256))) uint64_t g_qm_planes[QM_MAX_BLOCKS * QM_PLANES * 64];
-__device__ __attribute__((aligned(256))) uint32_t g_qm_meta[QM_MAX_BLOCKS * 3 * 16];
+// x in fp16 planes, written by k_qmm_xprep and read by k_qmm on the same stream.
+// A operands: [block][plane hi, lo][lane 0..63] 16 bytes each. Meta: 2^-s per
+// (chunk, column) (f32, NaN for a chunk with a non-finite value) at [chunk * 16 + j],
+// then the block sums of x' = x * 2^s at [QM_META_XS + block * 16 + j] (read for
+// Q4_1/Q5_1). Calls that overlap on one GPU race.
+__device__ __attribute__((aligned(256))) uint4 g_qm_a[QM_MAX_BLOCKS * 2 * 64];
+__device__ __attribute__((aligned(256))) float g_qm_meta[QM_META_XS + QM_MAX_BLOCKS * 16];
 
 template <int TYPE>
 constexpr bool rotated_even() {
     return TYPE == TRC_HIP_TYPE_Q4_0 || TYPE == TRC_HIP_TYPE_Q5_0 || TYPE == TRC_HIP_TYPE_Q8_0;
 }
 
-__device__ __forceinline__ uint32_t pack_bytes(const int* v) {
-    return (uint32_t) (v[0] & 0xFF) | ((uint32_t) (v[1] & 0xFF) << 8) | ((uint32_t) (v[2] & 0xFF) << 16) |
-           ((uint32_t) (v[3] & 0xFF) << 24);
-}
-
-// One thread per (block b, column j): it reads the block's 32 values, finds the
-// scale and writes the digit bytes of all four MFMA lanes j + 16g that carry
-// column j (no cross-lane traffic, so the kernel is one load and one store deep).
-__global__ __launch_bounds__(256) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk,
-                                                    int rot, int bias) {
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    const int b = t >> 4, j = t & 15;
-    if (b >= nblk) return;
-    float v[32];
-    if (j < N) {
-        const f4* col = (const f4*) (x + j * ldx + (int64_t) b * QK);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const f4 w = col[q];
-            v[4 * q] = w.x; v[4 * q + 1] = w.y; v[4 * q + 2] = w.z; v[4 * q + 3] = w.w;
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < 32; ++e) v[e] = 0.f;
-    }
-    float mx = 0.f, sm = 0.f;
+// One wave per (chunk of QM_CHB blocks, column j): lane l carries block
+// b = l / 4 of the chunk and lane group g = l % 4. It loads exactly the 8
+// elements of A entry (b, g) (the low elements e_p and e_p + 16), the wave's
+// largest |x| and finiteness give the chunk's scale 2^s, and the lane writes its
+// hi and lo entries. The block sums of x' (for Q4_1/Q5_1) are added over the
+// four lanes of a block. No reduction spans more than one wave.
+__global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot) {
+    const int ch = blockIdx.x >> 4, j = blockIdx.x & 15;  // columns past N get zeros
+    const int l = threadIdx.x, bl = l >> 2, g = l & 3;
+    const int b = ch * QM_CHB + bl;
+    const bool live = j < N && b < nblk;
+    const int c = ((b & 1) == 0 && rot) ? 2 : 0;
+    const int e0 = (c + 4 * g) & 15, e2 = (c + 4 * g + 2) & 15;  // e1 = e0 + 1, e3 = e2 + 1
+    const float2* blk = (const float2*) (x + (int64_t) (live ? j : 0) * ldx + (int64_t) (live ? b : 0) * QK);
+    const float2 z = {0.f, 0.f};
+    const float2 v01 = live ? blk[e0 >> 1] : z, v23 = live ? blk[e2 >> 1] : z;
+    const float2 w01 = live ? blk[(e0 + 16) >> 1] : z, w23 = live ? blk[(e2 + 16) >> 1] : z;
+    const float v[8] = {v01.x, v23.x, w01.x, w23.x, v01.y, v23.y, w01.y, w23.y};  // slot order
+    float mx = 0.f;
     int bad = 0;  // fmaxf drops NaN, so non-finite values are flagged separately
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
-        mx = fmaxf(mx, fabsf(v[e]));
-        sm += v[e];
-        bad |= !__builtin_isfinite(v[e]);
+    for (int k = 0; k < 8; ++k) {
+        mx = fmaxf(mx, fabsf(v[k]));
+        bad |= !__builtin_isfinite(v[k]);
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        bad |= __shfl_xor(bad, o, 64);
     }
     const bool finite = bad == 0;
     // mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^QM_XBITS
     const int s = (mx > 0.f && finite) ? QM_XBITS - __builtin_amdgcn_frexp_expf(mx) : 0;
-    int dg[QM_PLANES][32];
-    int sx = 0;
+    h8 hi, lo;
+    float sm = 0.f;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
-        const int X = finite ? (int) __builtin_rintf(__builtin_ldexpf(v[e], s)) : 0;
-        sx += X;
-        // balanced base-256 digits: X = d0 + 256 d1 (+ 65536 d2), d0, d1 in [-128, 127]
-        const int X1 = (X + 128) >> 8;
-        dg[0][e] = X - (X1 << 8);
-        if constexpr (QM_PLANES == 2) {
-            dg[1][e] = X1;  // |X1| <= 64
-        } else {
-            const int X2 = (X1 + 128) >> 8;
-            dg[1][e] = X1 - (X2 << 8);
-            dg[2][e] = X2;  // |X2| <= 32
-        }
+    for (int k = 0; k < 8; ++k) {
+        const float e = finite ? __builtin_ldexpf(v[k], s) : 0.f;
+        sm += e;
+        const _Float16 h = (_Float16) e;
+        hi[k] = h;
+        lo[k] = (_Float16) (e - (float) h);
     }
-    // lane group g feeds k = 8g..8g+7: elements E = (c + 4g + i) & 15 (i < 4), then 16 + E
-    const int c = (b & 1) ? 0 : rot;
-    uint64_t* dst = g_qm_planes + (int64_t) b * QM_PLANES * 64 + j;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-#pragma unroll
-        for (int p = 0; p < QM_PLANES; ++p) {
-            int lo[4], hi[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                // c is 0 or 2: select between two constant indices (no dynamic register indexing)
-                lo[i] = c ? dg[p][(2 + 4 * g + i) & 15] : dg[p][(4 * g + i) & 15];
-                hi[i] = c ? dg[p][16 + ((2 + 4 * g + i) & 15)] : dg[p][16 + ((4 * g + i) & 15)];
-            }
-            dst[64 * p + 16 * g] = (uint64_t) pack_bytes(lo) | ((uint64_t) pack_bytes(hi) << 32);
-        }
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    if (b < nblk) {
+        uint4* dst = g_qm_a + (int64_t) b * 2 * 64 + j + 16 * g;
+        dst[0] = __builtin_bit_cast(uint4, hi);
+        dst[64] = __builtin_bit_cast(uint4, lo);
+        if (g == 0) g_qm_meta[QM_META_XS + b * 16 + j] = sm;
     }
-    uint32_t* meta = g_qm_meta + b * 48 + j;
-    meta[0] = __builtin_bit_cast(uint32_t, finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf(""));
-    meta[16] = __builtin_bit_cast(uint32_t, sm);
-    meta[32] = (uint32_t) (-bias * sx);  // |.| <= 16 * 32 * 2^21 = 2^30
+    if (l == 0) g_qm_meta[ch * 16 + j] = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
 }
 
 // Per format: which dwords of a pair each lane loads (NW of them), in bytes
@@ -192,22 +174,60 @@ struct QmFmt<TRC_HIP_TYPE_Q8_0> {
     }
 };
 
-// Nibble bytes of a quant dword (low nibbles -> k 0..3, high -> k 4..7 of the
-// lane group), with the 5th bits of the 4 low / 4 high elements (bits 0-3 /
-// 4-7 of fifth). Values stay unsigned (0..31); a bias goes into the MFMA's
-// accumulator input instead.
-template <bool FIVE>
-__device__ __forceinline__ long nibbles(uint32_t w, uint32_t fifth) {
-    uint32_t lo = w & 0x0F0F0F0Fu;
-    uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+// fp16 B operand of one block for lane group g, in the k order e0, e2, e0+16,
+// e2+16, e1, e3, e1+16, e3+16 (e_p = element of quant byte p of the lane's dword).
+//   nibble formats: w = the lane's quant dword (byte p: low nibble e_p, high e_p+16),
+//     f5 = the 5th bits as bit p (e_p) and bit 4+p (e_p+16) (Q5_0/Q5_1),
+//     value q - BIAS with q = nibble (+ 16 * 5th bit);
+//   Q8_0: lo / hi = the lane's quant bytes of e_p / e_p + 16 (signed).
+// Masks and the fp16 magic number kept in VGPRs: gfx9 VOP3 encodes no literal,
+// so v_and_or_b32 needs its constants in registers (otherwise and + or).
+struct QmK {
+    uint32_t lo4, hi4, lo8, magic;
+};
+__device__ __forceinline__ QmK qm_consts() {
+    QmK k{0x000F000Fu, 0x00F000F0u, 0x00FF00FFu, 0x64006400u};
+    asm volatile("" : "+v"(k.lo4), "+v"(k.hi4), "+v"(k.lo8), "+v"(k.magic));
+    return k;
+}
+
+template <int BIAS, bool FIVE>
+__device__ __forceinline__ h8 qm_nibbles_f16(uint32_t w, uint32_t f5, const QmK& k) {
+    const uint32_t w8 = w >> 8;
+    uint32_t t0 = (w & k.lo4) | k.magic;   // 1024 + n: bytes 0, 2 low nibbles  (e0, e2)
+    uint32_t t1 = (w & k.hi4) | k.magic;   // 1024 + 16n: bytes 0, 2 high       (e0+16, e2+16)
+    uint32_t t2 = (w8 & k.lo4) | k.magic;  // bytes 1, 3 low                      (e1, e3)
+    uint32_t t3 = (w8 & k.hi4) | k.magic;  // bytes 1, 3 high                     (e1+16, e3+16)
     if constexpr (FIVE) {
-        // bit i of a 4-bit field -> bit 8i with one full-rate 24-bit multiply (a plain
-        // multiply would be folded with the shift into a quarter-rate 32-bit one),
-        // then to bit 4 of byte i
-        lo |= (__umul24(fifth & 0xFu, 0x00204081u) & 0x01010101u) << 4;
-        hi |= (__umul24((fifth >> 4) & 0xFu, 0x00204081u) & 0x01010101u) << 4;
+        // 5th bit of e_p -> bit 4 (+16 for the high half); of e_p+16 -> bit 8 (x16 scale)
+        // with one full-rate 24-bit multiply per pair: bits 0 and 2 of a field land
+        // on bits 4 and 20 (x 0x40010), bits 4 and 6 on bits 8 and 24 (x 0x40010 >> ...)
+        t0 |= __umul24(f5 & 0x5u, 0x40010u) & 0x00100010u;          // bits 0, 2 -> 4, 20
+        t2 |= __umul24((f5 >> 1) & 0x5u, 0x40010u) & 0x00100010u;   // bits 1, 3 -> 4, 20
+        t1 |= __umul24((f5 >> 4) & 0x5u, 0x40010u) << 4 & 0x01000100u;  // bits 4, 6 -> 8, 24
+        t3 |= __umul24((f5 >> 5) & 0x5u, 0x40010u) << 4 & 0x01000100u;  // bits 5, 7 -> 8, 24
     }
-    return (long) ((uint64_t) lo | ((uint64_t) hi << 32));
+    constexpr _Float16 LOW = (_Float16) (-(1024 + BIAS));        // 1024 + q  -> q - BIAS
+    constexpr _Float16 HIGH = (_Float16) (-(64 + BIAS));         // (1024 + 16q) / 16 -> q - BIAS
+    const h2 r0 = __builtin_bit_cast(h2, t0) + h2{LOW, LOW};
+    const h2 r1 = __builtin_bit_cast(h2, t1) * h2{(_Float16) 0.0625f, (_Float16) 0.0625f} + h2{HIGH, HIGH};
+    const h2 r2 = __builtin_bit_cast(h2, t2) + h2{LOW, LOW};
+    const h2 r3 = __builtin_bit_cast(h2, t3) * h2{(_Float16) 0.0625f, (_Float16) 0.0625f} + h2{HIGH, HIGH};
+    return h8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+}
+
+__device__ __forceinline__ h8 qm_bytes_f16(uint32_t lo, uint32_t hi, const QmK& k) {
+    const uint32_t ul = lo ^ 0x80808080u, uh = hi ^ 0x80808080u;  // q + 128 in every byte
+    const uint32_t t0 = (ul & k.lo8) | k.magic;         // bytes 0, 2 of lo (e0, e2)
+    const uint32_t t1 = (uh & k.lo8) | k.magic;         // bytes 0, 2 of hi (e0+16, e2+16)
+    const uint32_t t2 = ((ul >> 8) & k.lo8) | k.magic;  // bytes 1, 3 of lo (e1, e3)
+    const uint32_t t3 = ((uh >> 8) & k.lo8) | k.magic;  // bytes 1, 3 of hi (e1+16, e3+16)
+    constexpr _Float16 OFF = (_Float16) -1152.f;               // 1024 + 128 + q -> q
+    const h2 r0 = __builtin_bit_cast(h2, t0) + h2{OFF, OFF};
+    const h2 r1 = __builtin_bit_cast(h2, t1) + h2{OFF, OFF};
+    const h2 r2 = __builtin_bit_cast(h2, t2) + h2{OFF, OFF};
+    const h2 r3 = __builtin_bit_cast(h2, t3) + h2{OFF, OFF};
+    return h8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
 }
 
 // 5th bits of lane group g's elements, from a block's qh (rotated for c = 2).
@@ -218,50 +238,38 @@ __device__ __forceinline__ uint32_t rot2_halves(uint32_t qh) {
     return ((qh >> 2) & 0x3FFF3FFFu) | ((qh << 14) & 0xC000C000u);
 }
 
-// Digit combination a0 + 256 a1 + 65536 a2 as two v_lshl_add_u32: the empty
-// asm keeps the compiler from folding it into two shifts and a three-way add.
-// (A real inline-asm v_lshl_add would read the MFMA results without the wait
-// states the compiler inserts for its own instructions.)
-__device__ __forceinline__ uint32_t combine3(int a0, int a1, int a2) {
-    uint32_t t = (uint32_t) a0 + ((uint32_t) a1 << 8);
-    asm("" : "+v"(t));
-    return t + ((uint32_t) a2 << 16);
-}
-
 struct QmBlocks {
-    long B[2];       // B operands of the even and odd block
+    h8 B[2];         // B operands of the even and odd block
     uint32_t dm[2];  // d (low half) and m (high half, Q4_1/Q5_1) as fp16 bits
 };
 
 template <int TYPE>
-__device__ __forceinline__ QmBlocks qm_decode(const uint32_t* w, int g, uint32_t sel) {
+__device__ __forceinline__ QmBlocks qm_decode(const uint32_t* w, int g, uint32_t sel, const QmK& k) {
     QmBlocks r;
     if constexpr (TYPE == TRC_HIP_TYPE_Q4_0) {
-        r.B[0] = nibbles<false>(__builtin_amdgcn_perm(w[1], w[2], sel), 0);
-        r.B[1] = nibbles<false>(w[3], 0);
+        r.B[0] = qm_nibbles_f16<8, false>(__builtin_amdgcn_perm(w[1], w[2], sel), 0, k);
+        r.B[1] = qm_nibbles_f16<8, false>(w[3], 0, k);
         r.dm[0] = w[0] & 0xFFFFu;
         r.dm[1] = w[1] >> 16;
     } else if constexpr (TYPE == TRC_HIP_TYPE_Q4_1) {
-        r.B[0] = nibbles<false>(w[2], 0);
-        r.B[1] = nibbles<false>(w[3], 0);
+        r.B[0] = qm_nibbles_f16<0, false>(w[2], 0, k);
+        r.B[1] = qm_nibbles_f16<0, false>(w[3], 0, k);
         r.dm[0] = w[0];
         r.dm[1] = w[1];
     } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_0) {
         const uint32_t qh0 = __builtin_amdgcn_perm(w[1], w[0], 0x05040302u);
-        r.B[0] = nibbles<true>(__builtin_amdgcn_perm(w[2], w[4], sel), fifth_bits(rot2_halves(qh0), g));
-        r.B[1] = nibbles<true>(w[5], fifth_bits(w[3], g));
+        r.B[0] = qm_nibbles_f16<16, true>(__builtin_amdgcn_perm(w[2], w[4], sel), fifth_bits(rot2_halves(qh0), g), k);
+        r.B[1] = qm_nibbles_f16<16, true>(w[5], fifth_bits(w[3], g), k);
         r.dm[0] = w[0] & 0xFFFFu;
         r.dm[1] = w[2] >> 16;
     } else if constexpr (TYPE == TRC_HIP_TYPE_Q5_1) {
-        r.B[0] = nibbles<true>(w[4], fifth_bits(w[1], g));
-        r.B[1] = nibbles<true>(w[5], fifth_bits(w[3], g));
+        r.B[0] = qm_nibbles_f16<0, true>(w[4], fifth_bits(w[1], g), k);
+        r.B[1] = qm_nibbles_f16<0, true>(w[5], fifth_bits(w[3], g), k);
         r.dm[0] = w[0];
         r.dm[1] = w[2];
     } else {  // Q8_0
-        const uint32_t lo = __builtin_amdgcn_perm(w[1], w[3], sel);
-        const uint32_t hi = __builtin_amdgcn_perm(w[2], w[4], sel);
-        r.B[0] = (long) ((uint64_t) lo | ((uint64_t) hi << 32));
-        r.B[1] = (long) ((uint64_t) w[5] | ((uint64_t) w[6] << 32));
+        r.B[0] = qm_bytes_f16(__builtin_amdgcn_perm(w[1], w[3], sel), __builtin_amdgcn_perm(w[2], w[4], sel), k);
+        r.B[1] = qm_bytes_f16(w[5], w[6], k);
         r.dm[0] = w[0] & 0xFFFFu;
         r.dm[1] = w[2] >> 16;
     }
@@ -269,133 +277,145 @@ __device__ __forceinline__ QmBlocks qm_decode(const uint32_t* w, int g, uint32_t
 }
 
 constexpr int QM_CP = 8;       // pairs per K chunk (one per wave)
+static_assert(2 * QM_CP == QM_CHB, "the x scales follow the K chunks");
 constexpr int QM_RING = 3;     // chunks in flight: registers -> LDS ring depth
 
 // The x operands of one pair (two blocks) for this lane.
 struct QmX {
-    long xp[2][QM_PLANES];
-    f4 sc[2];
-    v4i aux[2];  // -BIAS * sum X (int, the first MFMA's accumulator input) or the block sums of x (float bits)
+    h8 a[2][2];  // [block][plane hi, lo]
+    f4 sc;       // 2^-s of the pair's chunk for the lane's 4 columns
+    f4 xs[2];    // block sums of x' for the lane's 4 columns (Q4_1/Q5_1)
 };
 
 template <int TYPE>
-__device__ __forceinline__ void qm_load_x(QmX& x, __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rm, uint32_t xo,
+__device__ __forceinline__ void qm_load_x(QmX& x, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rm, uint32_t ao,
                                           uint32_t mo, int p) {
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int b = 2 * p + h;
 #pragma unroll
-        for (int d = 0; d < QM_PLANES; ++d) {
-            x.xp[h][d] = __builtin_bit_cast(
-                long, __builtin_amdgcn_raw_buffer_load_b64(rx, xo, (b * QM_PLANES + d) * 512, 0));
+        for (int pl = 0; pl < 2; ++pl) {
+            x.a[h][pl] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(ra, ao, (b * 2 + pl) * 1024, 0));
         }
-        x.sc[h] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, b * 192, 0));
-        if constexpr (MIN || QmFmt<TYPE>::BIAS != 0) {
-            x.aux[h] = __builtin_bit_cast(
-                v4i, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, b * 192 + (MIN ? 64 : 128), 0));
+        if constexpr (MIN) {
+            x.xs[h] = __builtin_bit_cast(
+                f4, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, (QM_META_XS + b * 16) * 4, 0));
         }
     }
+    x.sc = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, (2 * p / QM_CHB) * 64, 0));
 }
 
 // One pair of all T tiles: quant dwords from the LDS chunk, x from registers.
 template <int TYPE, int T>
 __device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32_t (*lo)[QmFmt<TYPE>::NW],
-                                           const QmX& x, int g, uint32_t sel, f4* acc) {
+                                           const QmX& x, int g, uint32_t sel, const QmK& kc, f4* acc) {
     constexpr int NW = QmFmt<TYPE>::NW;
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
-    constexpr int BIAS = QmFmt<TYPE>::BIAS;
-    const v4i zero = {0, 0, 0, 0};
-    v4i c0[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) c0[h] = BIAS != 0 ? x.aux[h] : zero;
+    const f4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         uint32_t w[NW];
 #pragma unroll
         for (int i = 0; i < NW; ++i) w[i] = *(const uint32_t*) (lds_pair + lo[t][i]);
-        const QmBlocks q = qm_decode<TYPE>(w, g, sel);
+        const QmBlocks q = qm_decode<TYPE>(w, g, sel, kc);
+        f4 part = zero;  // the pair's sum in units of x' = x * 2^s
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            // sum_e (q_e - BIAS) X_e = [sum_e q_e P0_e - BIAS sum_e X_e] + 256 sum_e q_e P1_e + 65536 sum_e q_e P2_e
-            const v4i a0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x.xp[h][0], q.B[h], c0[h], 0, 0, 0);
-            const v4i a1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x.xp[h][1], q.B[h], zero, 0, 0, 0);
-            v4i a2 = zero;
-            if constexpr (QM_PLANES == 3) a2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x.xp[h][2], q.B[h], zero, 0, 0, 0);
+            // sum_e (q_e - BIAS) x'_e over both planes, exact products, fp32 sums
+            f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.a[h][0], q.B[h], zero, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.a[h][1], q.B[h], c, 0, 0, 0);
             const float d = half_bits_to_float(q.dm[h] & 0xFFFFu);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float qx;
-                if constexpr (QM_PLANES == 3 && TYPE == TRC_HIP_TYPE_Q8_0) {
-                    qx = __builtin_fmaf((float) a2[i], 65536.f, (float) (a0[i] + a1[i] * 256));
-                } else if constexpr (QM_PLANES == 3) {
-                    // modulo 2^32: the exact result fits in int32 (|q - bias| <= 31, |X| <= 2^21)
-                    // even where the partial sums with the bias term would not
-                    qx = (float) (int) combine3(a0[i], a1[i], a2[i]);
-                } else {
-                    qx = (float) (int) ((uint32_t) a0[i] + (uint32_t) a1[i] * 256u);
-                }
-                acc[t][i] = __builtin_fmaf(qx, d * x.sc[h][i], acc[t][i]);
-                if constexpr (MIN) {
+            for (int i = 0; i < 4; ++i) part[i] = __builtin_fmaf(d, c[i], part[i]);
+            if constexpr (MIN) {
+                const float mn = half_bits_to_float(q.dm[h] >> 16);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
                     // the element is copied out first: __builtin_bit_cast applied to a
                     // vector-element lvalue reads element 0 with this compiler
-                    const int xs_bits = x.aux[h][i];
-                    acc[t][i] = __builtin_fmaf(half_bits_to_float(q.dm[h] >> 16), __builtin_bit_cast(float, xs_bits),
-                                               acc[t][i]);
+                    const float xs = x.xs[h][i];
+                    part[i] = __builtin_fmaf(mn, xs, part[i]);
                 }
             }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float sc = x.sc[i];
+            acc[t][i] = __builtin_fmaf(sc, part[i], acc[t][i]);  // back to units of x
         }
     }
 }
 
-template <int TYPE, int T>
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maximum).
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(VM >= 0 && VM < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane
+// (buffer_load_dwordx4 ... lds; the LDS base goes through M0).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*) lds, 16, voff, soff, 0, 0);
+}
+
+template <int TYPE, int T, int ROUNDS>
 struct QmTile {
     static constexpr int PW = QmFmt<TYPE>::PW;
-    static constexpr int RB = QM_CP * PW * 4;         // bytes of one row in a chunk (a multiple of 16)
-    static constexpr int PITCH = RB + 16;             // LDS row pitch: rows start 4 banks apart
-    static constexpr int ROWS = 16 * T;
-    static constexpr int BUF = ROWS * PITCH;          // one chunk in LDS
-    static constexpr int PIECES = ROWS * (RB / 16);   // 16-byte pieces of a chunk
-    static constexpr int PPT = (PIECES + QM_WAVES * 64 - 1) / (QM_WAVES * 64);  // pieces per thread
+    static constexpr int RB = QM_CP * PW * 4;             // bytes of one row in a chunk (a multiple of 16)
+    static constexpr int SLOTS = ROUNDS * QM_WAVES * 64;   // 16-byte pieces one chunk buffer holds
+    static constexpr int BUF = SLOTS * 16;                 // one chunk buffer in LDS
 };
 
-template <int TYPE, int T>
+// R chunks of W stream from HBM straight into an LDS ring of R + 1 buffers
+// (buffer_load ... lds: no registers, no VALU), each chunk with the x operands
+// it needs loaded R chunks ahead into a register ring. Per chunk every wave
+// issues exactly ROUNDS + NA vector loads, so one vmcnt wait covers both: the
+// counter retires loads in issue order. Lanes past the workgroup's rows and the
+// chunks past the end re-read valid data; nothing reads their results.
+template <int TYPE, int T, int ROUNDS, int R>
 __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict__ W, int nblk, int64_t M,
                                                         int64_t nb1_w, float* __restrict__ y, int64_t ldy, int N,
                                                         int rows_per_wg) {
-    using TL = QmTile<TYPE, T>;
+    using TL = QmTile<TYPE, T, ROUNDS>;
     constexpr int NW = QmFmt<TYPE>::NW, PW = TL::PW;
-    static_assert(QM_RING * TL::BUF >= QM_WAVES * T * 64 * 16, "reduction buffer aliases the chunk ring");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[QM_RING * TL::BUF];
+    constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
+    constexpr int NA = MIN ? 7 : 5;  // x loads per chunk and wave (two blocks x two planes, scales, block sums)
+    static_assert((R + 1) * TL::BUF >= QM_WAVES * T * 64 * 16, "reduction buffer aliases the chunk ring");
+    static_assert((R + 1) * TL::BUF <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[(R + 1) * TL::BUF];
 
     // wave index as a scalar: the pair a wave computes and its buffer offsets are wave-uniform
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, m16 = lane & 15, g = lane >> 4;
     const int64_t r0 = (int64_t) blockIdx.x * rows_per_wg;
     const int64_t rend = r0 + rows_per_wg < M ? r0 + rows_per_wg : M;
+    const int rows = (int) (rend - r0);
     const int np = nblk / 2;
     const int nch = (np + QM_CP - 1) / QM_CP;
     const uint32_t sel = g < 3 ? 0x03020100u : 0x03020504u;
 
-    // The workgroup's rows as one buffer (the launcher keeps it below 2^31 bytes):
-    // loads of rows past M return zeros.
+    // The workgroup's rows as one buffer (the launcher keeps it below 2^31 bytes).
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        (void*) (W + r0 * nb1_w), (short) 0, (int) ((rend - r0) * nb1_w), QM_RSRC_WORD3);
+        (void*) (W + r0 * nb1_w), (short) 0, (int) ((int64_t) rows * nb1_w), QM_RSRC_WORD3);
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-        (void*) g_qm_planes, (short) 0, (int) sizeof(g_qm_planes), QM_RSRC_WORD3);
+        (void*) g_qm_a, (short) 0, (int) sizeof(g_qm_a), QM_RSRC_WORD3);
     const __amdgpu_buffer_rsrc_t rm =
         __builtin_amdgcn_make_buffer_rsrc((void*) g_qm_meta, (short) 0, (int) sizeof(g_qm_meta), QM_RSRC_WORD3);
 
-    // cooperative chunk copy: thread piece k -> row k / (RB/16), 16 bytes at (k % (RB/16)) * 16
-    uint32_t go[TL::PPT], so[TL::PPT];
-    bool pv[TL::PPT];
+    // LDS slot k * 512 + thread = row q / RB16, piece q % RB16 of a chunk. Row r's
+    // 16-byte pieces sit rotated by r, so the 16 rows a lane group reads in one
+    // instruction fall on different banks; slots past the rows re-read piece 0.
+    constexpr int RB16 = TL::RB / 16;
+    uint32_t go[ROUNDS];
 #pragma unroll
-    for (int k = 0; k < TL::PPT; ++k) {
-        const int q = (int) threadIdx.x + k * QM_WAVES * 64;
-        const int row = q / (TL::RB / 16), pc = q % (TL::RB / 16);
-        pv[k] = q < TL::PIECES;
-        go[k] = (uint32_t) (row * nb1_w) + pc * 16;
-        so[k] = row * TL::PITCH + pc * 16;
+    for (int k = 0; k < ROUNDS; ++k) {
+        int q = k * QM_WAVES * 64 + (int) threadIdx.x;
+        if (q >= rows * RB16) q = 0;
+        const int r = q / RB16, slot = q % RB16;
+        go[k] = (uint32_t) (r * nb1_w) + (uint32_t) ((slot + RB16 - r % RB16) % RB16) * 16;
     }
     // this lane's quant dwords of its wave's pair, per tile, as LDS byte offsets within a chunk
     int off[NW];
@@ -403,55 +423,70 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     uint32_t lo[T][NW];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
+        const int r = 16 * t + m16;
 #pragma unroll
-        for (int i = 0; i < NW; ++i) lo[t][i] = (16 * t + m16) * TL::PITCH + wave * PW * 4 + 4 * off[i];
+        for (int i = 0; i < NW; ++i) {
+            const int d = wave * PW + off[i];  // dword of the row chunk
+            lo[t][i] = r * TL::RB + ((d / 4 + r) % RB16) * 16 + (d % 4) * 4;
+        }
     }
-    const uint32_t xo = lane * 8, mo = 16 * g;
+    const uint32_t xo = lane * 16, mo = 16 * g;
+    const QmK kc = qm_consts();
 
     f4 acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
-    uint4 wr[QM_RING][TL::PPT];
-    QmX xr[QM_RING];
-    auto load_chunk = [&](int s, int c) {
-        const int cc = c < nch ? c : nch - 1;  // past the end: repeat the last chunk (unused)
+    QmX xr[R];
+    // W of chunk c (or of the last one past the end) -> LDS buffer b
+    auto load_w = [&](int c, int b) {
+        const int cc = c < nch ? c : nch - 1;
+        uint8_t* dst = lds + b * TL::BUF + wave * 1024;
 #pragma unroll
-        for (int k = 0; k < TL::PPT; ++k) {
-            if (pv[k]) {
-                wr[s][k] = __builtin_bit_cast(
-                    uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, go[k], cc * TL::RB, 0));
-            }
-        }
-        const int p = cc * QM_CP + wave;
-        qm_load_x<TYPE>(xr[s], rx, rm, xo, mo, p < np ? p : np - 1);
-    };
-    auto store_chunk = [&](int s, int buf) {
-#pragma unroll
-        for (int k = 0; k < TL::PPT; ++k) {
-            if (pv[k]) *(uint4*) (lds + buf * TL::BUF + so[k]) = wr[s][k];
+        for (int k = 0; k < ROUNDS; ++k) {
+            dma16(rw, dst + k * QM_WAVES * 1024, go[k], cc * TL::RB);
         }
     };
-    auto step = [&](int c, int s) {
-        // chunk c sits in LDS buffer s and its x in xr[s]; chunk c+1 goes to LDS, c+3 is fetched
-        if (c * QM_CP + wave < np) qm_compute<TYPE, T>(lds + s * TL::BUF, lo, xr[s], g, sel, acc);
-        store_chunk((s + 1) % QM_RING, (s + 1) % QM_RING);
-        load_chunk(s, c + QM_RING);
-        __syncthreads();
+    // x operands of this wave's pair of chunk c -> xr[xs]
+    auto load_x = [&](int c, int xs) {
+        const int p = (c < nch ? c : nch - 1) * QM_CP + wave;
+        qm_load_x<TYPE>(xr[xs], rx, rm, xo, mo, p < np ? p : np - 1);
     };
-
+    // Step c. Loads go out per chunk as W then x, so once at most (R - 1) chunks'
+    // loads are outstanding, chunk c's W (this wave's part) and x have landed;
+    // the barrier makes every wave's part of the W chunk visible. Chunk c + R's W
+    // goes to the buffer of chunk c - 1, which every wave finished before the
+    // barrier; its x goes to xr[c % R] once chunk c is computed.
+    auto step = [&](int c, int xs) {
+        wait_vmcnt<(R - 1) * (ROUNDS + NA)>();
+        // a bare s_barrier: __syncthreads' workgroup fence would also wait for
+        // every LDS-bound load in flight, i.e. drain the ring each step. The
+        // empty asm keeps the compiler from moving LDS accesses across it.
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        load_w(c + R, (c + R) % (R + 1));
+        if (c < nch && c * QM_CP + wave < np) {
+            qm_compute<TYPE, T>(lds + (c % (R + 1)) * TL::BUF, lo, xr[xs], g, sel, kc, acc);
+        }
+        load_x(c + R, xs);
+    };
+    // prologue in chunk order (the first wait counts on chunk 0's loads being the oldest)
 #pragma unroll
-    for (int s = 0; s < QM_RING; ++s) load_chunk(s, s);
-    store_chunk(0, 0);
-    __syncthreads();
-    int c = 0;
-    for (; c + QM_RING <= nch; c += QM_RING) {
-        step(c, 0);
-        step(c + 1, 1);
-        step(c + 2, 2);
+    for (int i = 0; i < R; ++i) {
+        load_w(i, i);
+        load_x(i, i);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    if (c < nch) step(c, 0);
-    if (c + 1 < nch) step(c + 1, 1);
+    // whole groups of R steps, so that every path issues the same loads (steps
+    // past the last chunk compute nothing) and the compiler's own wait counts
+    // for the x registers stay exact
+    for (int c = 0; c < nch; c += R) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) step(c + i, i);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
 
     // sum over the waves (fixed order) through the now idle chunk ring
     f4* red = (f4*) lds;
@@ -472,21 +507,37 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     }
 }
 
-template <int TYPE, int T>
+template <int TYPE, int T, int ROUNDS, int R>
 int launch_t(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
              hipStream_t s) {
     const int64_t grid = (M + rows - 1) / rows;
-    hipLaunchKernelGGL((k_qmm<TYPE, T>), dim3((unsigned) grid), dim3(QM_WAVES * 64), 0, s, (const uint8_t*) wq,
-                       nblk, M, (int64_t) nb1_w, y, (int64_t) (nb1_y / sizeof(float)), N, rows);
+    hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R>), dim3((unsigned) grid), dim3(QM_WAVES * 64), 0, s,
+                       (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, y, (int64_t) (nb1_y / sizeof(float)), N, rows);
     return check_launch("qmm");
+}
+
+// ROUNDS = 16-byte pieces of a chunk per thread, rounded up; the ring depth R
+// keeps (R + 1) chunk buffers within the LDS.
+template <int TYPE, int T>
+int launch_rounds(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
+                  hipStream_t s) {
+    constexpr int RB16 = QM_CP * QmFmt<TYPE>::PW * 4 / 16;
+    const int rounds = (rows * RB16 + QM_WAVES * 64 - 1) / (QM_WAVES * 64);
+    switch (rounds) {
+        case 1: return launch_t<TYPE, T, 1, 4>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
+        case 2: return launch_t<TYPE, T, 2, 4>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
+        case 3: return launch_t<TYPE, T, 3, 4>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
+        case 4: return launch_t<TYPE, T, 4, 3>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
+        default: return launch_t<TYPE, T, 5, 3>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
+    }
 }
 
 template <int TYPE>
 int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
                size_t nb1_y, hipStream_t s) {
-    hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) ((nblk * 16 + 255) / 256)), dim3(256), 0, s, x,
-                       (int64_t) (nb1_x / sizeof(float)), N, nblk, rotated_even<TYPE>() ? 2 : 0,
-                       QmFmt<TYPE>::BIAS);
+    const int nchunks = (nblk + QM_CHB - 1) / QM_CHB;
+    hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) (nchunks * 16)), dim3(64), 0, s, x, (int64_t) (nb1_x / sizeof(float)),
+                       N, nblk, rotated_even<TYPE>() ? 2 : 0);
     const int rc = check_launch("qmm_xprep");
     if (rc != TRC_HIP_OK) return rc;
     // rows per workgroup: one workgroup per CU when M allows, 8-row granularity, at most 64
@@ -496,10 +547,10 @@ int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x
     if (rows > 64) rows = 64;
     const int T = (int) ((rows + 15) / 16);
     switch (T) {
-        case 1: return launch_t<TYPE, 1>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
-        case 2: return launch_t<TYPE, 2>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
-        case 3: return launch_t<TYPE, 3>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
-        default: return launch_t<TYPE, 4>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
+        case 1: return launch_rounds<TYPE, 1>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
+        case 2: return launch_rounds<TYPE, 2>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
+        case 3: return launch_rounds<TYPE, 3>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
+        default: return launch_rounds<TYPE, 4>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
     }
 }
 
