@@ -348,6 +348,9 @@ def main():
                 else:
                     r, _, _ = qmatvec_case(H, synth, timer, t, K, M, N, s, w)
                 extra["qmatvec"][f"{name} N={N}"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+        # skinny GEMM at the top of the fused range (one pass over W per 16 columns)
+        r, _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 64, s, w)
+        extra["qmatvec"]["q4_0 N=64"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
         extra["dequant_4096x11008"] = {}
         for name, t in H.QUANT_TYPES.items():
             r = dequant_case(H, synth, timer, t, 4096 * 11008 // 32, s, w)

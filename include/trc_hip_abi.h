@@ -59,8 +59,9 @@ enum trc_hip_type {
     TRC_HIP_TYPE_Q8_0 = 8
 };
 
-/* Largest activation batch (columns of src1) the fused quantized matvec takes. */
-#define TRC_HIP_QMATVEC_MAX_N 16
+/* Largest activation batch (columns of src1) the fused quantized matvec takes
+ * (skinny GEMM up to 64 columns; W is read once per 16 columns). */
+#define TRC_HIP_QMATVEC_MAX_N 64
 
 /* Fields of DeviceProps (include/traincpp/trc_backend.h:14-28) plus what the
  * kernels' launch heuristics need. */

@@ -86,7 +86,7 @@ def test_argument_errors(hip):
     x = empty(4096)
     y = empty(4096)
     with pytest.raises(H.HipError) as e:
-        H.qmatvec(H.TYPE_Q4_0, w.ptr, 64, 4, 36, x.ptr, 17, 256, y.ptr, 16)
+        H.qmatvec(H.TYPE_Q4_0, w.ptr, 64, 4, 36, x.ptr, H.QMATVEC_MAX_N + 1, 256, y.ptr, 16)
     assert e.value.code == H.E_SHAPE
     with pytest.raises(H.HipError) as e:
         H.qmatvec(H.TYPE_Q4_0, w.ptr, 48, 4, 36, x.ptr, 1, 192, y.ptr, 16)  # K % 32
@@ -96,7 +96,7 @@ def test_argument_errors(hip):
     assert e.value.code == H.E_ALIGN
 
 
-# The int8 matrix-core kernel (qmm.hip) takes 2 <= N <= 16 with a multiple of
+# The fp16 matrix-core kernel (qmm.hip) takes 2 <= N <= 16 with a multiple of
 # 8 blocks per row (K % 256 == 0), in chunks of 16 blocks; the cases below pin
 # its layouts, grid shapes, partial last chunks and numerics. Other block
 # counts above exercise the fallback kernels.
@@ -194,6 +194,33 @@ def test_mfma_block_limit(hip, nblk):
     announce(f"qmm limit nblk={nblk}")
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, nblk))
     X = synth.normal(nblk, K * N).reshape(1, 1, N, K)
+    got = gpu_qmatvec(t, raw, K, M, X)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert O.row_l2_error(got, want) <= TOL
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("N", [17, 31, 33, 48, 64])
+def test_skinny_gemm_wide(hip, name, N):
+    """N up to 64: one fused pass over W per 16 columns (the last slice may be a
+    single column, which takes the batch-1 kernel)."""
+    t = TYPES[name]
+    K, M = 32 * 40, 203
+    announce(f"qmatvec wide {name} N={N}")
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 300 + N + t))
+    X = synth.normal(400 + N, K * N).reshape(1, 1, N, K)
+    got = gpu_qmatvec(t, raw, K, M, X, x_pad=8, y_pad=5)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert O.row_l2_error(got, want) <= TOL
+
+
+def test_config2_q4_0_n64(hip):
+    """Configuration 2's weight (Q4_0 14336 x 4096) against 64 columns."""
+    t = TYPES["q4_0"]
+    K, M, N = 4096, 14336, 64
+    announce("qmatvec cfg2 q4_0 N=64")
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, synth.config_seed(2, t)))
+    X = synth.normal(synth.config_seed(2, 164), K * N).reshape(1, 1, N, K)
     got = gpu_qmatvec(t, raw, K, M, X)
     want = oracle_qmatvec(t, raw, K, M, X)
     assert O.row_l2_error(got, want) <= TOL

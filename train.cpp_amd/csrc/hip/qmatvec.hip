@@ -972,6 +972,17 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
 
 int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
                    size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream) {
+    if (N > 16) {
+        // skinny GEMM beyond 16 columns: one fused pass over W per 16 columns
+        // (the launches run in order on the stream, so they can share the x scratch)
+        for (int64_t c0 = 0; c0 < N; c0 += 16) {
+            const int64_t n = N - c0 < 16 ? N - c0 : 16;
+            const int rc = launch_qmatvec(type, wq, K, M, nb1_w, (const float*) ((const uint8_t*) x + c0 * nb1_x), n,
+                                          nb1_x, (float*) ((uint8_t*) y + c0 * nb1_y), nb1_y, stream);
+            if (rc != TRC_HIP_OK) return rc;
+        }
+        return TRC_HIP_OK;
+    }
     const bool wide = type == TRC_HIP_TYPE_Q4_1 || type == TRC_HIP_TYPE_Q5_1;
     const unsigned walign = wide ? 3u : 1u;
     if ((((uintptr_t) wq) & walign) != 0 || (nb1_w & walign) != 0) {

@@ -15,7 +15,7 @@ LIB_PATH = LIB_DIR / "libtrc_hip.so"
 TYPE_F32, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q5_0, TYPE_Q5_1, TYPE_Q8_0 = 0, 2, 3, 6, 7, 8
 QUANT_TYPES = {"q4_0": TYPE_Q4_0, "q4_1": TYPE_Q4_1, "q5_0": TYPE_Q5_0, "q5_1": TYPE_Q5_1, "q8_0": TYPE_Q8_0}
 BLOCK_BYTES = {TYPE_Q4_0: 18, TYPE_Q4_1: 20, TYPE_Q5_0: 22, TYPE_Q5_1: 24, TYPE_Q8_0: 34}
-QMATVEC_MAX_N = 16
+QMATVEC_MAX_N = 64
 
 OK, E_INVALID, E_SHAPE, E_ALIGN, E_NO_DEVICE, E_FORCED = 0, -1, -2, -3, -4, -5
 
