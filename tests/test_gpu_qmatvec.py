@@ -70,9 +70,9 @@ def test_all_formats_small(hip, name, N):
 
 @pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("K,M", [(32, 1), (64, 3), (4096, 64), (11008, 257)])
-def test_edge_shapes_and_padded_columns(hip, name, K, M):
+@pytest.mark.parametrize("N", [2, 4])
+def test_edge_shapes_and_padded_columns(hip, name, K, M, N):
     t = TYPES[name]
-    N = 4
     announce(f"qmatvec edge {name} K={K} M={M}")
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 5 + K + M))
     X = synth.normal(K + M, K * N).reshape(1, 1, N, K)
@@ -149,12 +149,12 @@ def test_mfma_dynamic_range(hip, name):
 
 
 @pytest.mark.parametrize("name", ["q4_0", "q5_1", "q8_0"])
-@pytest.mark.parametrize("N", [1, 4])
+@pytest.mark.parametrize("N", [1, 2, 4])
 @pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
 def test_nonfinite_x(hip, name, N, bad):
     """A non-finite x element makes its column non-finite, as in the reference
     (the fixed-point kernels return NaN there); the other columns are unaffected.
-    Covers the integer-dot (N = 1), streaming (Q8_0, N = 1) and int8 MFMA kernels."""
+    Covers the integer-dot (N = 1, 2) and fp16 MFMA (N = 4) kernels."""
     t = TYPES[name]
     K, M = 256, 40
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 8))

@@ -790,16 +790,18 @@ __device__ __forceinline__ float wave_sum_lane63(float v) {
     return v;
 }
 
-template <int TYPE, int RPW>
+// NC columns of x (1 or 2) share one pass over W: each row's quant words are
+// decoded once and met by every column's digit planes (48 registers per column).
+template <int TYPE, int RPW, int NC>
 __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __restrict__ W, int64_t nblk, int64_t M,
-                                                     int64_t nb1_w, const float* __restrict__ x,
-                                                     float* __restrict__ y) {
+                                                     int64_t nb1_w, const float* __restrict__ x, int64_t ldx,
+                                                     float* __restrict__ y, int64_t ldy) {
     constexpr int BYTES = block_bytes(TYPE);
     constexpr int PW = QdFmt<TYPE>::PAIR_WORDS;
     constexpr int PF = QD_PREFETCH < RPW ? QD_PREFETCH : RPW;
-    __shared__ __attribute__((aligned(16))) uint32_t planes[(QD_CH / 2) * QD_PSTRIDE];
-    __shared__ float scale_l[QD_CH];
-    __shared__ float xsum_l[QD_CH];
+    __shared__ __attribute__((aligned(16))) uint32_t planes[NC][(QD_CH / 2) * QD_PSTRIDE];
+    __shared__ float scale_l[NC][QD_CH];
+    __shared__ float xsum_l[NC][QD_CH];
 
     const int lane = threadIdx.x & 63;
     const int64_t wave_id = (int64_t) blockIdx.x * QD_WAVES + (threadIdx.x >> 6);
@@ -819,9 +821,11 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         roff[r] = (row < M ? row : M - 1) * nb1_w;
     }
 
-    float acc[RPW];
+    float acc[NC][RPW];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = 0.f;
+    for (int n = 0; n < NC; ++n)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) acc[n][r] = 0.f;
 
     const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
     uint32_t w[RPW][PW];
@@ -837,89 +841,109 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         };
         // x is loaded first (vector loads return in issue order), then the
         // weight stream starts so that it overlaps the conversion of x
-        f4 xv[4];
-        QdX4 xn;
-        if constexpr (qd_nibble_path<TYPE>()) {
-            qd_load_x_n4<TYPE == TRC_HIP_TYPE_Q4_0>(x + c * QD_CH * QK, cb, xn);
-        } else {
-            qd_load_x(x + c * QD_CH * QK, cb, xv);
+        f4 xv[NC][4];
+        QdX4 xn[NC];
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            if constexpr (qd_nibble_path<TYPE>()) {
+                qd_load_x_n4<TYPE == TRC_HIP_TYPE_Q4_0>(x + n * ldx + c * QD_CH * QK, cb, xn[n]);
+            } else {
+                qd_load_x(x + n * ldx + c * QD_CH * QK, cb, xv[n]);
+            }
         }
 #pragma unroll
         for (int r = 0; r < PF; ++r) issue(r);
         // keep these loads above the prologue and its barrier
         __builtin_amdgcn_sched_barrier(0);
         if (c > 0) __syncthreads();  // previous chunk's planes are no longer read
-        if constexpr (qd_nibble_path<TYPE>()) {
-            qd_prologue_n4(xn, cb, planes, scale_l, xsum_l);
-        } else {
-            qd_prologue<TYPE == TRC_HIP_TYPE_Q8_0>(xv, cb, planes, scale_l, xsum_l);
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            if constexpr (qd_nibble_path<TYPE>()) {
+                qd_prologue_n4(xn[n], cb, planes[n], scale_l[n], xsum_l[n]);
+            } else {
+                qd_prologue<TYPE == TRC_HIP_TYPE_Q8_0>(xv[n], cb, planes[n], scale_l[n], xsum_l[n]);
+            }
         }
         __syncthreads();
 
-        // this lane's pair: the plane words of blocks A and B (24 each). Nibble
-        // path: A at dwords 0-23, B at 24-47. Byte path: plane p of A at
+        // this lane's pair: the plane words of blocks A and B (24 each) per column.
+        // Nibble path: A at dwords 0-23, B at 24-47. Byte path: plane p of A at
         // 16p..16p+7 and of B at 16p+8..16p+15.
-        uint32_t PA[24], PB[24];
-        const uint32_t* src = planes + pl * QD_PSTRIDE;
+        uint32_t PA[NC][24], PB[NC][24];
+        float sc[NC][2], xs[NC][2];
 #pragma unroll
-        for (int k = 0; k < 12; ++k) {
-            const uint4 v = *(const uint4*) (src + 4 * k);
-            uint32_t* dst;
-            if constexpr (qd_nibble_path<TYPE>()) {
-                dst = k < 6 ? &PA[4 * k] : &PB[4 * (k - 6)];
-            } else {
-                const int p = k >> 2, g = k & 3;
-                dst = g < 2 ? &PA[8 * p + 4 * g] : &PB[8 * p + 4 * (g - 2)];
+        for (int n = 0; n < NC; ++n) {
+            const uint32_t* src = planes[n] + pl * QD_PSTRIDE;
+#pragma unroll
+            for (int k = 0; k < 12; ++k) {
+                const uint4 v = *(const uint4*) (src + 4 * k);
+                uint32_t* dst;
+                if constexpr (qd_nibble_path<TYPE>()) {
+                    dst = k < 6 ? &PA[n][4 * k] : &PB[n][4 * (k - 6)];
+                } else {
+                    const int p = k >> 2, g = k & 3;
+                    dst = g < 2 ? &PA[n][8 * p + 4 * g] : &PB[n][8 * p + 4 * (g - 2)];
+                }
+                dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
             }
-            dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+            sc[n][0] = scale_l[n][2 * pl];
+            sc[n][1] = scale_l[n][2 * pl + 1];
+            xs[n][0] = xsum_l[n][2 * pl];
+            xs[n][1] = xsum_l[n][2 * pl + 1];
         }
-        const float sc[2] = {scale_l[2 * pl], scale_l[2 * pl + 1]};
-        const float xs[2] = {xsum_l[2 * pl], xsum_l[2 * pl + 1]};
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
             if (r + PF < RPW) issue(r + PF);
             __builtin_amdgcn_sched_barrier(0);  // row r + PF stays in flight during row r
-            const float v = qd_pair<TYPE>(w[r], PA, PB, sc, xs);
-            acc[r] += mine ? v : 0.f;
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                const float v = qd_pair<TYPE>(w[r], PA[n], PB[n], sc[n], xs[n]);
+                acc[n][r] += mine ? v : 0.f;
+            }
             // after the last chunk a row is final: reduce and store it while the
             // next rows' loads are in flight, so the wave ends one reduction
             // after its last row instead of RPW
             if (c == nchunks - 1) {
-                const float sum = wave_sum_lane63(acc[r]);
                 const int64_t row = wave_id + r * n_waves;
-                if (lane == 63 && row < M) y[row] = sum;
+#pragma unroll
+                for (int n = 0; n < NC; ++n) {
+                    const float sum = wave_sum_lane63(acc[n][r]);
+                    if (lane == 63 && row < M) y[n * ldy + row] = sum;
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
 
-template <int TYPE, int RPW>
-int launch_dot_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y, hipStream_t s) {
+template <int TYPE, int RPW, int NC>
+int launch_dot_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, float* y,
+                   size_t nb1_y, hipStream_t s) {
     const int64_t waves = (M + RPW - 1) / RPW;
     const int64_t grid = (waves + QD_WAVES - 1) / QD_WAVES;
-    hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s, (const uint8_t*) wq,
-                       nblk, M, (int64_t) nb1_w, x, y);
+    hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s,
+                       (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, (int64_t) (nb1_x / sizeof(float)), y,
+                       (int64_t) (nb1_y / sizeof(float)));
     return check_launch("qmatvec_dot");
 }
 
-template <int TYPE>
-int launch_qmatvec_dot(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y,
-                       hipStream_t s) {
+template <int TYPE, int NC>
+int launch_qmatvec_dot(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, float* y,
+                       size_t nb1_y, hipStream_t s) {
     // spread the rows evenly over 8 waves per CU (2 per SIMD), at most QD_RMAX each
     const int64_t target_waves = (int64_t) device_cus() * 8;
     int64_t rpw = (M + target_waves - 1) / target_waves;
     if (rpw > QD_RMAX) rpw = QD_RMAX;
     if (rpw < 1) rpw = 1;
     switch (rpw) {
-        case 1: return launch_dot_rpw<TYPE, 1>(wq, nblk, M, nb1_w, x, y, s);
-        case 2: return launch_dot_rpw<TYPE, 2>(wq, nblk, M, nb1_w, x, y, s);
-        case 3: return launch_dot_rpw<TYPE, 3>(wq, nblk, M, nb1_w, x, y, s);
-        case 4: return launch_dot_rpw<TYPE, 4>(wq, nblk, M, nb1_w, x, y, s);
-        case 5: return launch_dot_rpw<TYPE, 5>(wq, nblk, M, nb1_w, x, y, s);
-        case 6: return launch_dot_rpw<TYPE, 6>(wq, nblk, M, nb1_w, x, y, s);
-        case 7: return launch_dot_rpw<TYPE, 7>(wq, nblk, M, nb1_w, x, y, s);
-        default: return launch_dot_rpw<TYPE, 8>(wq, nblk, M, nb1_w, x, y, s);
+        case 1: return launch_dot_rpw<TYPE, 1, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 2: return launch_dot_rpw<TYPE, 2, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 3: return launch_dot_rpw<TYPE, 3, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 4: return launch_dot_rpw<TYPE, 4, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 5: return launch_dot_rpw<TYPE, 5, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 6: return launch_dot_rpw<TYPE, 6, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 7: return launch_dot_rpw<TYPE, 7, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        default: return launch_dot_rpw<TYPE, 8, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
     }
 }
 
@@ -946,13 +970,15 @@ template <int TYPE>
 int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N, size_t nb1_x,
                 float* y, size_t nb1_y, hipStream_t s) {
     const int64_t nblk = K / QK;
-    // 2 <= N <= 16: int8 matrix-core kernel (qmm.hip)
+    // N = 1, 2: integer-dot kernel (one pass over W for both columns; a third
+    // column's planes would not fit the registers); pairs of blocks start on
+    // 4-byte boundaries and x columns on 16-byte ones
+    const bool dot_ok = nblk % 2 == 0 && (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0 &&
+                        (((uintptr_t) x) & 15u) == 0 && (nb1_x & 15u) == 0;
+    if (dot_ok && N == 1) return launch_qmatvec_dot<TYPE, 1>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+    if (dot_ok && N == 2) return launch_qmatvec_dot<TYPE, 2>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+    // 3 <= N <= 16 (and N = 2 off the dot kernel's alignment): fp16 matrix-core kernel (qmm.hip)
     if (qmm_supported(K, N, wq, nb1_w)) return launch_qmm(TYPE, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s);
-    // N = 1 integer-dot kernel: pairs of blocks start on 4-byte boundaries
-    if (N == 1 && nblk % 2 == 0 && (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0 &&
-        (((uintptr_t) x) & 15u) == 0) {
-        return launch_qmatvec_dot<TYPE>(wq, nblk, M, nb1_w, x, y, s);
-    }
     // N = 1 streaming kernel: needs 16-byte aligned rows and row chunks
     if (N == 1 && nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0) {
         // Q8_0 blocks are twice as large: a 4-row tile already fills the registers.
