@@ -37,15 +37,18 @@
 // writes the x planes in the same order, so each lane loads its A operand of a
 // block with one 16-byte load per plane.
 //
-// Work split: a workgroup (8 waves) owns up to 64 rows (T tiles of 16) and
+// Work split: a workgroup (8 waves) owns up to 112 rows (T tiles of 16) and
 // walks K in chunks of 8 pairs. Each chunk is copied by the whole workgroup
-// with coalesced 16-byte buffer loads (loads landing in MFMA layout directly
-// would touch 16 rows per instruction and swamp the L1 with tag lookups),
-// three chunks ahead in registers, into a 3-buffer LDS ring; wave w computes
-// pair w of the chunk for all T tiles, so its x operands are loaded once per
-// chunk and reused over the tiles. The partial sums are added across the
-// waves through LDS in a fixed order, so results are deterministic. Rows per
-// workgroup are chosen so the grid covers every CU once when M allows.
+// with coalesced 16-byte buffer loads straight into LDS (loads landing in MFMA
+// layout directly would touch 16 rows per instruction and swamp the L1 with
+// tag lookups), 3 or 4 chunks ahead, into a ring of R + 1 buffers whose rows
+// are padded to an odd number of 16-byte pieces (conflict-free reads); wave w
+// computes pair w of the chunk for all T tiles, so its x operands are loaded
+// once per chunk and reused over the tiles. The partial sums are added across
+// the waves through LDS in a fixed order, so results are deterministic. Rows
+// per workgroup are chosen so the grid covers every CU once when M allows;
+// below 8 rows per CU, K is split in two parts whose sums meet in y by float
+// atomic adds (0 + a + b, the same in either order).
 #include "common.h"
 
 namespace trc_hip {
@@ -57,6 +60,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 constexpr int QM_MAX_BLOCKS = 2048;  // K <= 65536
 constexpr int QM_WAVES = 8;
 constexpr int QM_CHB = 16;            // blocks per K chunk (8 pairs, one per wave)
+constexpr int QM_LDS = 160 * 1024;      // LDS per workgroup
 constexpr int QM_XBITS = 14;          // max|x'| < 2^14 keeps hi and its rounding inside fp16
 constexpr int QM_META_XS = QM_MAX_BLOCKS / QM_CHB * 16;  // block sums follow the chunk scales
 constexpr uint32_t QM_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
@@ -80,9 +84,19 @@ constexpr bool rotated_even() {
 // largest |x| and finiteness give the chunk's scale 2^s, and the lane writes its
 // hi and lo entries. The block sums of x' (for Q4_1/Q5_1) are added over the
 // four lanes of a block. No reduction spans more than one wave.
-__global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot) {
+//
+// A launch split over K adds two partial sums into y, so then (y0 != nullptr)
+// the wave also clears its share of column j of y: rows
+// [ch * per, (ch + 1) * per) with per = ceil(M / chunks).
+__global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot,
+                                                   float* __restrict__ y0, int64_t ldy, int64_t M) {
     const int ch = blockIdx.x >> 4, j = blockIdx.x & 15;  // columns past N get zeros
     const int l = threadIdx.x, bl = l >> 2, g = l & 3;
+    if (y0 != nullptr && j < N) {
+        const int64_t nchunks = gridDim.x >> 4, per = (M + nchunks - 1) / nchunks;
+        const int64_t a = ch * per, e = a + per < M ? a + per : M;
+        for (int64_t m = a + l; m < e; m += 64) y0[j * ldy + m] = 0.f;
+    }
     const int b = ch * QM_CHB + bl;
     const bool live = j < N && b < nblk;
     const int c = ((b & 1) == 0 && rot) ? 2 : 0;
@@ -306,45 +320,66 @@ __device__ __forceinline__ void qm_load_x(QmX& x, __amdgpu_buffer_rsrc_t ra, __a
     x.sc = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, (2 * p / QM_CHB) * 64, 0));
 }
 
-// One pair of all T tiles: quant dwords from the LDS chunk, x from registers.
-template <int TYPE, int T>
-__device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32_t (*lo)[QmFmt<TYPE>::NW],
-                                           const QmX& x, int g, uint32_t sel, const QmK& kc, f4* acc) {
-    constexpr int NW = QmFmt<TYPE>::NW;
+// The scaled sums of one tile's pair: per block d * sum_e (q_e - BIAS) x'_e (+ m *
+// sum_e x'_e for Q4_1/Q5_1) in units of x' = x * 2^s, then back to units of x.
+template <int TYPE>
+__device__ __forceinline__ void qm_scale(const f4 (&c)[2], const uint32_t (&dm)[2], const QmX& x, f4& acc) {
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
-    const f4 zero = {0.f, 0.f, 0.f, 0.f};
+    f4 part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        uint32_t w[NW];
+    for (int h = 0; h < 2; ++h) {
+        const float d = half_bits_to_float(dm[h] & 0xFFFFu);
 #pragma unroll
-        for (int i = 0; i < NW; ++i) w[i] = *(const uint32_t*) (lds_pair + lo[t][i]);
-        const QmBlocks q = qm_decode<TYPE>(w, g, sel, kc);
-        f4 part = zero;  // the pair's sum in units of x' = x * 2^s
+        for (int i = 0; i < 4; ++i) part[i] = __builtin_fmaf(d, c[h][i], part[i]);
+        if constexpr (MIN) {
+            const float mn = half_bits_to_float(dm[h] >> 16);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            // sum_e (q_e - BIAS) x'_e over both planes, exact products, fp32 sums
-            f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.a[h][0], q.B[h], zero, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.a[h][1], q.B[h], c, 0, 0, 0);
-            const float d = half_bits_to_float(q.dm[h] & 0xFFFFu);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) part[i] = __builtin_fmaf(d, c[i], part[i]);
-            if constexpr (MIN) {
-                const float mn = half_bits_to_float(q.dm[h] >> 16);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // the element is copied out first: __builtin_bit_cast applied to a
-                    // vector-element lvalue reads element 0 with this compiler
-                    const float xs = x.xs[h][i];
-                    part[i] = __builtin_fmaf(mn, xs, part[i]);
-                }
+            for (int i = 0; i < 4; ++i) {
+                // the element is copied out first: __builtin_bit_cast applied to a
+                // vector-element lvalue reads element 0 with this compiler
+                const float xs = x.xs[h][i];
+                part[i] = __builtin_fmaf(mn, xs, part[i]);
             }
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float sc = x.sc[i];
-            acc[t][i] = __builtin_fmaf(sc, part[i], acc[t][i]);  // back to units of x
-        }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float sc = x.sc[i];
+        acc[i] = __builtin_fmaf(sc, part[i], acc[i]);
+    }
+}
+
+// One pair of all T tiles: quant dwords from the LDS chunk, x from registers.
+// Software-pipelined over the tiles: every quant dword is read first, then
+// step t issues tile t's four MFMAs and, while they run, decodes tile t + 1
+// and scales tile t - 1, whose MFMA results are one step old. The scheduling
+// barriers keep the compiler from folding the steps back into a dependent chain.
+template <int TYPE, int T>
+__device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32_t* lo,
+                                           const QmX& x, int g, uint32_t sel, const QmK& kc, f4* acc) {
+    constexpr int NW = QmFmt<TYPE>::NW, RB = QM_CP * QmFmt<TYPE>::PW * 4;  // bytes of one row in a chunk
+    const f4 zero = {0.f, 0.f, 0.f, 0.f};
+    uint32_t w[T][NW];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) w[t][i] = *(const uint32_t*) (lds_pair + lo[i] + t * 16 * (RB + 16));
+    }
+    QmBlocks q[T];
+    f4 c[T][2];
+    q[0] = qm_decode<TYPE>(w[0], g, sel, kc);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        // sum_e (q_e - BIAS) x'_e over both planes: exact products, fp32 sums
+#pragma unroll
+        for (int h = 0; h < 2; ++h) c[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.a[h][0], q[t].B[h], zero, 0, 0, 0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) c[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.a[h][1], q[t].B[h], c[t][h], 0, 0, 0);
+        if (t + 1 < T) q[t + 1] = qm_decode<TYPE>(w[t + 1], g, sel, kc);
+        if (t >= 1) qm_scale<TYPE>(c[t - 1], q[t - 1].dm, x, acc[t - 1]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    qm_scale<TYPE>(c[T - 1], q[T - 1].dm, x, acc[T - 1]);
 }
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
@@ -365,8 +400,11 @@ template <int TYPE, int T, int ROUNDS>
 struct QmTile {
     static constexpr int PW = QmFmt<TYPE>::PW;
     static constexpr int RB = QM_CP * PW * 4;             // bytes of one row in a chunk (a multiple of 16)
-    static constexpr int SLOTS = ROUNDS * QM_WAVES * 64;   // 16-byte pieces one chunk buffer holds
-    static constexpr int BUF = SLOTS * 16;                 // one chunk buffer in LDS
+    static constexpr int LS = RB + 16;                     // LDS row stride: the row and one spare piece
+    static constexpr int FILL = ROUNDS * QM_WAVES * 64 * 16;  // bytes the copy of one chunk writes
+    // one chunk buffer in LDS: the copied pieces, and at least all 16T rows, so
+    // that the reads of the last tile's rows past the workgroup's stay inside it
+    static constexpr int BUF = FILL > 16 * T * LS ? FILL : 16 * T * LS;
 };
 
 // R chunks of W stream from HBM straight into an LDS ring of R + 1 buffers
@@ -375,16 +413,20 @@ struct QmTile {
 // issues exactly ROUNDS + NA vector loads, so one vmcnt wait covers both: the
 // counter retires loads in issue order. Lanes past the workgroup's rows and the
 // chunks past the end re-read valid data; nothing reads their results.
+//
+// K split: blockIdx.y selects chunks [c0, c0 + part_chunks) of K. With more than
+// one part (gridDim.y == 2) the parts' sums meet in y, which k_qmm_xprep
+// cleared, by float atomic adds; 0 + a + b rounds the same in either order.
 template <int TYPE, int T, int ROUNDS, int R>
 __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict__ W, int nblk, int64_t M,
                                                         int64_t nb1_w, float* __restrict__ y, int64_t ldy, int N,
-                                                        int rows_per_wg) {
+                                                        int rows_per_wg, int part_chunks) {
     using TL = QmTile<TYPE, T, ROUNDS>;
     constexpr int NW = QmFmt<TYPE>::NW, PW = TL::PW;
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
     constexpr int NA = MIN ? 7 : 5;  // x loads per chunk and wave (two blocks x two planes, scales, block sums)
     static_assert((R + 1) * TL::BUF >= QM_WAVES * T * 64 * 16, "reduction buffer aliases the chunk ring");
-    static_assert((R + 1) * TL::BUF <= 160 * 1024, "LDS");
+    static_assert((R + 1) * TL::BUF <= QM_LDS, "LDS");
     __shared__ __attribute__((aligned(16))) uint8_t lds[(R + 1) * TL::BUF];
 
     // wave index as a scalar: the pair a wave computes and its buffer offsets are wave-uniform
@@ -395,6 +437,8 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     const int rows = (int) (rend - r0);
     const int np = nblk / 2;
     const int nch = (np + QM_CP - 1) / QM_CP;
+    const int c0 = blockIdx.y * part_chunks;                             // this part's first chunk
+    const int nl = part_chunks < nch - c0 ? part_chunks : nch - c0;      // and its chunk count (>= 1)
     const uint32_t sel = g < 3 ? 0x03020100u : 0x03020504u;
 
     // The workgroup's rows as one buffer (the launcher keeps it below 2^31 bytes).
@@ -405,30 +449,30 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     const __amdgpu_buffer_rsrc_t rm =
         __builtin_amdgcn_make_buffer_rsrc((void*) g_qm_meta, (short) 0, (int) sizeof(g_qm_meta), QM_RSRC_WORD3);
 
-    // LDS slot k * 512 + thread = row q / RB16, piece q % RB16 of a chunk. Row r's
-    // 16-byte pieces sit rotated by r, so the 16 rows a lane group reads in one
-    // instruction fall on different banks; slots past the rows re-read piece 0.
-    constexpr int RB16 = TL::RB / 16;
+    // LDS slot k * 512 + thread = row q / LS16, piece q % LS16 of a chunk: rows
+    // sit TL::LS = RB + 16 bytes apart, an odd number of 16-byte pieces, so the
+    // 16 rows a lane group reads in one instruction fall on 16 different 4-bank
+    // groups (64 banks of 4 bytes) and every tile has the same layout at a fixed
+    // offset. The spare piece of a row re-reads the row's last piece, and slots
+    // past the rows re-read piece 0; nothing reads either.
+    constexpr int RB16 = TL::RB / 16, LS16 = RB16 + 1;
     uint32_t go[ROUNDS];
 #pragma unroll
     for (int k = 0; k < ROUNDS; ++k) {
         int q = k * QM_WAVES * 64 + (int) threadIdx.x;
-        if (q >= rows * RB16) q = 0;
-        const int r = q / RB16, slot = q % RB16;
-        go[k] = (uint32_t) (r * nb1_w) + (uint32_t) ((slot + RB16 - r % RB16) % RB16) * 16;
+        if (q >= rows * LS16) q = 0;
+        const int r = q / LS16, slot = q % LS16;
+        go[k] = (uint32_t) (r * nb1_w) + (uint32_t) (slot < RB16 ? slot : RB16 - 1) * 16;
     }
-    // this lane's quant dwords of its wave's pair, per tile, as LDS byte offsets within a chunk
+    // this lane's quant dwords of its wave's pair in tile 0, as LDS byte offsets
+    // within a chunk (tile t adds 16 * t rows)
     int off[NW];
     QmFmt<TYPE>::offsets(g, off);
-    uint32_t lo[T][NW];
+    uint32_t lo[NW];
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const int r = 16 * t + m16;
-#pragma unroll
-        for (int i = 0; i < NW; ++i) {
-            const int d = wave * PW + off[i];  // dword of the row chunk
-            lo[t][i] = r * TL::RB + ((d / 4 + r) % RB16) * 16 + (d % 4) * 4;
-        }
+    for (int i = 0; i < NW; ++i) {
+        const int d = wave * PW + off[i];  // dword of the row chunk
+        lo[i] = m16 * TL::LS + d * 4;
     }
     const uint32_t xo = lane * 16, mo = 16 * g;
     const QmK kc = qm_consts();
@@ -438,18 +482,18 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
     QmX xr[R];
-    // W of chunk c (or of the last one past the end) -> LDS buffer b
+    // W of the part's chunk c (or of its last one past the end) -> LDS buffer b
     auto load_w = [&](int c, int b) {
-        const int cc = c < nch ? c : nch - 1;
+        const int cc = c0 + (c < nl ? c : nl - 1);
         uint8_t* dst = lds + b * TL::BUF + wave * 1024;
 #pragma unroll
         for (int k = 0; k < ROUNDS; ++k) {
             dma16(rw, dst + k * QM_WAVES * 1024, go[k], cc * TL::RB);
         }
     };
-    // x operands of this wave's pair of chunk c -> xr[xs]
+    // x operands of this wave's pair of the part's chunk c -> xr[xs]
     auto load_x = [&](int c, int xs) {
-        const int p = (c < nch ? c : nch - 1) * QM_CP + wave;
+        const int p = (c0 + (c < nl ? c : nl - 1)) * QM_CP + wave;
         qm_load_x<TYPE>(xr[xs], rx, rm, xo, mo, p < np ? p : np - 1);
     };
     // Step c. Loads go out per chunk as W then x, so once at most (R - 1) chunks'
@@ -466,7 +510,7 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         load_w(c + R, (c + R) % (R + 1));
-        if (c < nch && c * QM_CP + wave < np) {
+        if (c < nl && (c0 + c) * QM_CP + wave < np) {
             qm_compute<TYPE, T>(lds + (c % (R + 1)) * TL::BUF, lo, xr[xs], g, sel, kc, acc);
         }
         load_x(c + R, xs);
@@ -481,7 +525,7 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     // whole groups of R steps, so that every path issues the same loads (steps
     // past the last chunk compute nothing) and the compiler's own wait counts
     // for the x registers stay exact
-    for (int c = 0; c < nch; c += R) {
+    for (int c = 0; c < nl; c += R) {
 #pragma unroll
         for (int i = 0; i < R; ++i) step(c + i, i);
     }
@@ -500,58 +544,125 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     for (int w = 1; w < QM_WAVES; ++w) sum += red[(w * T + t) * 64 + lane];
     const int64_t m = r0 + 16 * t + m16;
     if (m >= rend) return;
+    if (gridDim.y == 1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int j = 4 * g + i;
-        if (j < N) y[j * ldy + m] = sum[i];
+        for (int i = 0; i < 4; ++i) {
+            const int j = 4 * g + i;
+            if (j < N) y[j * ldy + m] = sum[i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = 4 * g + i;
+            if (j < N) __hip_atomic_fetch_add(y + j * ldy + m, sum[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
 template <int TYPE, int T, int ROUNDS, int R>
-int launch_t(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
-             hipStream_t s) {
+int launch_t(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows, int parts,
+             int part_chunks, hipStream_t s) {
     const int64_t grid = (M + rows - 1) / rows;
-    hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R>), dim3((unsigned) grid), dim3(QM_WAVES * 64), 0, s,
-                       (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, y, (int64_t) (nb1_y / sizeof(float)), N, rows);
+    hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R>), dim3((unsigned) grid, (unsigned) parts), dim3(QM_WAVES * 64), 0, s,
+                       (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, y, (int64_t) (nb1_y / sizeof(float)), N, rows,
+                       part_chunks);
     return check_launch("qmm");
 }
 
-// ROUNDS = 16-byte pieces of a chunk per thread, rounded up; the ring depth R
-// keeps (R + 1) chunk buffers within the LDS.
+// 16-byte LDS pieces of one row's chunk: the row and one spare.
+template <int TYPE>
+constexpr int qm_ls16() {
+    return QM_CP * QmFmt<TYPE>::PW * 4 / 16 + 1;
+}
+// One chunk buffer (QmTile's BUF) for T tiles and ROUNDS pieces per thread, and
+// the ring depth R it allows: R + 1 buffers within the LDS, R = 4 or 3.
+template <int TYPE>
+constexpr int qm_buf(int t, int rounds) {
+    const int fill = rounds * QM_WAVES * 64 * 16, pad = 16 * t * qm_ls16<TYPE>() * 16;
+    return fill > pad ? fill : pad;
+}
+template <int TYPE>
+constexpr int qm_ring(int t, int rounds) {
+    return 5 * qm_buf<TYPE>(t, rounds) <= QM_LDS ? 4 : 3;
+}
+constexpr int qm_rounds(int rows, int ls16) {
+    return (rows * ls16 + QM_WAVES * 64 - 1) / (QM_WAVES * 64);
+}
+// The most rows per workgroup (a multiple of 8, at most 112) whose ring of 4
+// buffers fits; the buffer grows with the rows, so every smaller count fits too.
+template <int TYPE>
+constexpr int qm_max_rows() {
+    int r = 112;
+    while (4 * qm_buf<TYPE>((r + 15) / 16, qm_rounds(r, qm_ls16<TYPE>())) > QM_LDS) r -= 8;
+    return r;
+}
+
+// ROUNDS = 16-byte LDS pieces of a chunk per thread, rounded up. Rows come in
+// multiples of 8, so T tiles hold 16T - 8 or 16T rows and ROUNDS takes one of
+// two values.
 template <int TYPE, int T>
 int launch_rounds(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
-                  hipStream_t s) {
-    constexpr int RB16 = QM_CP * QmFmt<TYPE>::PW * 4 / 16;
-    const int rounds = (rows * RB16 + QM_WAVES * 64 - 1) / (QM_WAVES * 64);
-    switch (rounds) {
-        case 1: return launch_t<TYPE, T, 1, 4>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
-        case 2: return launch_t<TYPE, T, 2, 4>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
-        case 3: return launch_t<TYPE, T, 3, 4>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
-        case 4: return launch_t<TYPE, T, 4, 3>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
-        default: return launch_t<TYPE, T, 5, 3>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, s);
+                  int parts, int part_chunks, hipStream_t s) {
+    constexpr int LS16 = qm_ls16<TYPE>();
+    constexpr int LO = qm_rounds(16 * T - 8, LS16), HI = qm_rounds(16 * T, LS16);
+    const int rounds = qm_rounds(rows, LS16);
+    if (rounds <= LO) {
+        return launch_t<TYPE, T, LO, qm_ring<TYPE>(T, LO)>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks,
+                                                           s);
     }
+    if constexpr (16 * T <= qm_max_rows<TYPE>()) {  // 16T rows is within the cap
+        return launch_t<TYPE, T, HI, qm_ring<TYPE>(T, HI)>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks,
+                                                           s);
+    } else {
+        return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
+    }
+}
+
+template <int TYPE, int T>
+int launch_tiles(int t, const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
+                 int parts, int part_chunks, hipStream_t s) {
+    if constexpr (T > (qm_max_rows<TYPE>() + 15) / 16) {
+        return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
+    } else {
+        if (t == T) return launch_rounds<TYPE, T>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, s);
+        return launch_tiles<TYPE, T + 1>(t, wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, s);
+    }
+}
+
+// Work split. Rows per workgroup: one workgroup per CU when M allows, in
+// multiples of 8, at most qm_max_rows. When even 8-row workgroups leave CUs
+// idle (M < 8 per CU), K is split in two parts, which doubles the workgroups
+// and halves the chunks each one walks.
+struct QmPlan {
+    int rows, parts, part_chunks;
+};
+template <int TYPE>
+QmPlan qm_plan(int nblk, int64_t M) {
+    const int nch = (nblk / 2 + QM_CP - 1) / QM_CP;
+    const int64_t cus = device_cus();
+    QmPlan p;
+    p.parts = nch >= 2 && (M + 7) / 8 < cus ? 2 : 1;
+    p.part_chunks = (nch + p.parts - 1) / p.parts;
+    p.parts = (nch + p.part_chunks - 1) / p.part_chunks;
+    int64_t rows = (M * p.parts + cus - 1) / cus;
+    rows = (rows + 7) / 8 * 8;
+    if (rows > qm_max_rows<TYPE>()) rows = qm_max_rows<TYPE>();
+    p.rows = (int) rows;
+    return p;
 }
 
 template <int TYPE>
 int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
                size_t nb1_y, hipStream_t s) {
+    const QmPlan p = qm_plan<TYPE>(nblk, M);
     const int nchunks = (nblk + QM_CHB - 1) / QM_CHB;
     hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) (nchunks * 16)), dim3(64), 0, s, x, (int64_t) (nb1_x / sizeof(float)),
-                       N, nblk, rotated_even<TYPE>() ? 2 : 0);
+                       N, nblk, rotated_even<TYPE>() ? 2 : 0, p.parts > 1 ? y : nullptr,
+                       (int64_t) (nb1_y / sizeof(float)), M);
     const int rc = check_launch("qmm_xprep");
     if (rc != TRC_HIP_OK) return rc;
-    // rows per workgroup: one workgroup per CU when M allows, 8-row granularity, at most 64
-    const int64_t cus = device_cus();
-    int64_t rows = (M + cus - 1) / cus;
-    rows = (rows + 7) / 8 * 8;
-    if (rows > 64) rows = 64;
-    const int T = (int) ((rows + 15) / 16);
-    switch (T) {
-        case 1: return launch_rounds<TYPE, 1>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
-        case 2: return launch_rounds<TYPE, 2>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
-        case 3: return launch_rounds<TYPE, 3>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
-        default: return launch_rounds<TYPE, 4>(wq, nblk, M, nb1_w, y, nb1_y, N, (int) rows, s);
-    }
+    return launch_tiles<TYPE, 1>((p.rows + 15) / 16, wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts, p.part_chunks,
+                                 s);
 }
 
 }  // namespace
