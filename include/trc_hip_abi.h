@@ -149,8 +149,8 @@ int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b,
  *   W : `type` blocks, ne = [K, M]; row m starts at wq + m*nb1_w bytes
  *   x : F32, ne = [K, N]; column n starts at x + n*nb1_x bytes (x[k] contiguous)
  *   y : F32, ne = [M, N]; column n starts at y + n*nb1_y bytes (y[m] contiguous)
- * with K % 32 == 0 and 1 <= N <= TRC_HIP_QMATVEC_MAX_N. The blocks are decoded
- * in registers and never written out as F32. There is no counterpart in the
+ * with K % 32 == 0 and 1 <= N <= TRC_HIP_QMATVEC_MAX_N; y must not overlap W or
+ * x. The blocks are decoded in registers and never written out as F32. There is no counterpart in the
  * reference: its CPU path rejects quantized mul_mat (src/ops/trc_ops.cpp:368)
  * and the equivalent result is gguf_tensor_to_f32 followed by F32 mul_mat. */
 int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w,
