@@ -8,15 +8,19 @@
 // Numerics. Within one 32-element block b of one row m
 //   sum_e (q_e*d + mn) * x_e,j = d * sum_e (q_e - bias) * x_e,j + mn * sum_e x_e,j.
 // The integer quants q_e - bias (|.| <= 128) are exact in fp16. x is converted
-// once per call (k_qmm_xprep): every column j is scaled by a power of two 2^s_j
-// so that max|x'| < 2^14, and x' = x * 2^s_j is split into two fp16 planes,
-// hi = fp16(x') and lo = fp16(x' - hi), about 22 significant bits. Both planes
-// go through the MFMA into one fp32 accumulator (every product of an 11-bit
-// and a 9-bit integer is exact), so a block needs one fused multiply-add by d
-// per output; 2^-s_j is applied once at the end. Elements more than 2^28 below
-// their column's largest |x| fall below fp16's range and drop out; their share
-// of the column's outputs is below FP32's own rounding. A column holding Inf
-// or NaN comes out NaN.
+// once per call (k_qmm_xprep): every chunk of 16 blocks of every column j is
+// scaled by a power of two 2^s so that its max|x'| < 2^14, and x' = x * 2^s is
+// split into two fp16 planes, hi = fp16(x') and lo = fp16(x' - hi), about 22
+// significant bits. Both planes go through the MFMA into one fp32 accumulator
+// (every product of an 11-bit and a 9-bit integer is exact), so a block needs
+// one fused multiply-add by d per output, and each pair's sum is scaled back by
+// its chunk's 2^-s once. An element keeps ~22 bits of its own magnitude down to
+// 2^17 below its chunk's largest |x|; below that its absolute error stays under
+// 2^-39 of that largest |x|, so outputs carry FP32-level error. A chunk holding
+// Inf or NaN makes its column come out NaN. (One scale per column would save
+// the per-pair rescaling, but finding a column's largest |x| takes one
+// workgroup per column, which made the pre-pass ~2 us slower than the
+// rescaling saves.)
 //
 // Quants to fp16 without a conversion instruction: a nibble n OR'ed into the
 // mantissa of 1024.0 (0x6400) is the fp16 value 1024 + n, and at bits 4-7 it
