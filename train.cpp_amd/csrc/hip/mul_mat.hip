@@ -17,6 +17,8 @@
 //     the dst stores are 128-byte runs when dst is ne0-contiguous.
 //   - K advances in BK-deep slabs staged in LDS as [k][row] (row = i or j,
 //     contiguous), read by the MFMA feed with 32 consecutive floats per half-wave.
+//     BK is 16 for 128x128 tiles and 32 for 64x64 tiles, whose waves would
+//     otherwise run only 8 MFMAs between two barriers.
 //   - Each operand is loaded by one of three loaders chosen on the host from
 //     its strides: K_CONTIG (nb0 == 4: float4 along k, the layout of weights and
 //     activations), R_CONTIG (nb1 == 4: float4 along i/j, the layout of the
@@ -30,7 +32,6 @@ namespace trc_hip {
 namespace {
 
 constexpr int MM_THREADS = 256;
-constexpr int BK = 16;
 
 enum LoadMode { K_CONTIG = 0, R_CONTIG = 1, GENERIC = 2 };
 
@@ -47,7 +48,7 @@ struct MMArgs {
 
 // Loads a ROWS x BK slab (rows = i for src0, j for src1) of one operand into
 // registers, then stores it to LDS as lds[k * LD + row].
-template <int MODE, int ROWS>
+template <int MODE, int ROWS, int BK>
 struct SlabLoader {
     static constexpr int LD = ROWS + 4;
     static constexpr int PER = ROWS * BK / MM_THREADS;  // floats per thread
@@ -130,13 +131,13 @@ struct SlabLoader {
     }
 };
 
-template <int WI, int WJ, int TI, int TJ, int AMODE, int BMODE>
+template <int WI, int WJ, int TI, int TJ, int BK, int AMODE, int BMODE>
 __global__ __launch_bounds__(MM_THREADS) void k_mul_mat(MMArgs p) {
     static_assert(WI * WJ * 64 == MM_THREADS, "four waves per workgroup");
     constexpr int BM = WI * TI * 32;  // tile extent along i
     constexpr int BN = WJ * TJ * 32;  // tile extent along j
-    using LA = SlabLoader<AMODE, BM>;
-    using LB = SlabLoader<BMODE, BN>;
+    using LA = SlabLoader<AMODE, BM, BK>;
+    using LB = SlabLoader<BMODE, BN, BK>;
     __shared__ __attribute__((aligned(16))) float As[BK * LA::LD];
     __shared__ __attribute__((aligned(16))) float Bs[BK * LB::LD];
 
@@ -235,21 +236,21 @@ int pick_mode(const trc_hip_tensor& t, int64_t rows) {
     return GENERIC;
 }
 
-template <int WI, int WJ, int TI, int TJ, int AM, int BMO>
+template <int WI, int WJ, int TI, int TJ, int BK, int AM, int BMO>
 int launch_cfg(MMArgs& p, int64_t planes, hipStream_t stream) {
     constexpr int BM = WI * TI * 32, BN = WJ * TJ * 32;
     p.tiles_i = (p.M + BM - 1) / BM;
     p.tiles_j = (p.N + BN - 1) / BN;
     const int64_t grid = p.tiles_i * p.tiles_j * planes;
     if (grid > 0x7FFFFFFF) return fail(TRC_HIP_E_SHAPE, "mul_mat: %lld workgroups exceed one launch", (long long) grid);
-    hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, AM, BMO>), dim3((unsigned) grid), dim3(MM_THREADS), 0, stream, p);
+    hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, BK, AM, BMO>), dim3((unsigned) grid), dim3(MM_THREADS), 0, stream, p);
     return check_launch("mul_mat_f32");
 }
 
-template <int WI, int WJ, int TI, int TJ>
+template <int WI, int WJ, int TI, int TJ, int BK>
 int dispatch_modes(MMArgs& p, int am, int bm, int64_t planes, hipStream_t s) {
 #define TRC_MM_CASE(A, B) \
-    if (am == A && bm == B) return launch_cfg<WI, WJ, TI, TJ, A, B>(p, planes, s);
+    if (am == A && bm == B) return launch_cfg<WI, WJ, TI, TJ, BK, A, B>(p, planes, s);
     TRC_MM_CASE(K_CONTIG, K_CONTIG)
     TRC_MM_CASE(K_CONTIG, R_CONTIG)
     TRC_MM_CASE(K_CONTIG, GENERIC)
@@ -286,8 +287,8 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
     // Large tiles when they still give every CU at least two workgroups;
     // otherwise 64x64 tiles to fill the chip.
     const int64_t big_tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128) * planes;
-    if (big_tiles >= 512) return dispatch_modes<2, 2, 2, 2>(p, am, bm, planes, stream);
-    return dispatch_modes<2, 2, 1, 1>(p, am, bm, planes, stream);
+    if (big_tiles >= 512) return dispatch_modes<2, 2, 2, 2, 16>(p, am, bm, planes, stream);
+    return dispatch_modes<2, 2, 1, 1, 32>(p, am, bm, planes, stream);
 }
 
 }  // namespace trc_hip
