@@ -311,6 +311,10 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time a 256 MiB device copy (reference for the traffic counters)")
+    ap.add_argument("--only", choices=["dequant", "mul_mat", "qmm"],
+                    help="only time one hot path and print its figures (for counter runs): dequant = the five "
+                         "formats on configuration 1, mul_mat = configurations 3 and 4, qmm = Q4_0 N=16 on "
+                         "configuration 2")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; multi-GPU runs are not part of this "
@@ -326,6 +330,18 @@ def main():
     K, M = 4096, 14336
     if args.calibrate_copy:
         print(json.dumps({"calibration": "copy", **copy_calibration(H, timer, args.steps, args.warmup)}), flush=True)
+        return
+    if args.only:
+        part = {"only": args.only}
+        if args.only == "dequant":
+            for name, t in H.QUANT_TYPES.items():
+                part[name] = dequant_case(H, synth, timer, t, 4096 * 11008 // 32, args.steps, args.warmup)
+        elif args.only == "mul_mat":
+            part["cfg3"] = mul_mat_config3(H, synth, timer, args.steps, args.warmup)
+            part["cfg4"] = mul_mat_config4(H, synth, timer, args.steps, args.warmup)
+        else:
+            part["q4_0 N=16"], _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 16, args.steps, args.warmup)
+        print(json.dumps(part), flush=True)
         return
 
     t_wall = time.perf_counter()
