@@ -364,7 +364,7 @@ def main():
                 else:
                     r, _, _ = qmatvec_case(H, synth, timer, t, K, M, N, s, w)
                 extra["qmatvec"][f"{name} N={N}"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
-        # skinny GEMM at the top of the fused range (one pass over W per 16 columns)
+        # skinny GEMM at the top of the fused range (one pass over W per 32 columns)
         r, _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 64, s, w)
         extra["qmatvec"]["q4_0 N=64"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
         extra["dequant_4096x11008"] = {}

@@ -60,7 +60,7 @@ enum trc_hip_type {
 };
 
 /* Largest activation batch (columns of src1) the fused quantized matvec takes
- * (skinny GEMM up to 64 columns; W is read once per 16 columns). */
+ * (skinny GEMM up to 64 columns; W is read once per 32 columns). */
 #define TRC_HIP_QMATVEC_MAX_N 64
 
 /* Fields of DeviceProps (include/traincpp/trc_backend.h:14-28) plus what the

@@ -977,7 +977,7 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
                         (((uintptr_t) x) & 15u) == 0 && (nb1_x & 15u) == 0;
     if (dot_ok && N == 1) return launch_qmatvec_dot<TYPE, 1>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
     if (dot_ok && N == 2) return launch_qmatvec_dot<TYPE, 2>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
-    // 3 <= N <= 16 (and N = 2 off the dot kernel's alignment): fp16 matrix-core kernel (qmm.hip)
+    // 3 <= N <= 32 (and N = 2 off the dot kernel's alignment): fp16 matrix-core kernel (qmm.hip)
     if (qmm_supported(K, N, wq, nb1_w)) return launch_qmm(TYPE, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s);
     // N = 1 streaming kernel: needs 16-byte aligned rows and row chunks
     if (N == 1 && nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0) {
@@ -998,11 +998,13 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
 
 int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
                    size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream) {
-    if (N > 16) {
-        // skinny GEMM beyond 16 columns: one fused pass over W per 16 columns
-        // (the launches run in order on the stream, so they can share the x scratch)
-        for (int64_t c0 = 0; c0 < N; c0 += 16) {
-            const int64_t n = N - c0 < 16 ? N - c0 : 16;
+    if (N > 16 && !(N <= 32 && qmm_supported(K, N, wq, nb1_w))) {
+        // skinny GEMM beyond the columns one launch carries: one fused pass over W
+        // per 32 columns on the matrix-core kernel, else per 16 (the launches run
+        // in order on the stream, so they can share the x scratch)
+        const int64_t step = qmm_supported(K, 32, wq, nb1_w) ? 32 : 16;
+        for (int64_t c0 = 0; c0 < N; c0 += step) {
+            const int64_t n = N - c0 < step ? N - c0 : step;
             const int rc = launch_qmatvec(type, wq, K, M, nb1_w, (const float*) ((const uint8_t*) x + c0 * nb1_x), n,
                                           nb1_x, (float*) ((uint8_t*) y + c0 * nb1_y), nb1_y, stream);
             if (rc != TRC_HIP_OK) return rc;

@@ -1,5 +1,7 @@
-// H2 for 2 <= N <= 16 columns: fused dequant x skinny GEMM on the fp16 matrix
-// cores (v_mfma_f32_16x16x32_f16).
+// H2 for 2 <= N <= 32 columns: fused dequant x skinny GEMM on the fp16 matrix
+// cores (v_mfma_f32_16x16x32_f16). Columns come in tiles of 16; one launch
+// carries one or two tiles (NT), so every weight is read and decoded once per
+// 32 columns.
 //
 // Result to reproduce: gguf_tensor_to_f32 (src/io/trc_gguf.cpp:966-1049,
 // dequantize_q* :320-417) followed by compute_mul_mat
@@ -66,23 +68,26 @@ constexpr int QM_WAVES = 8;
 constexpr int QM_CHB = 16;            // blocks per K chunk (8 pairs, one per wave)
 constexpr int QM_LDS = 160 * 1024;      // LDS per workgroup
 constexpr int QM_XBITS = 14;          // max|x'| < 2^14 keeps hi and its rounding inside fp16
-constexpr int QM_META_XS = QM_MAX_BLOCKS / QM_CHB * 16;  // block sums follow the chunk scales
+constexpr int QM_NT = 2;               // column tiles of 16 that one pass over W can carry
+constexpr int QM_COLS = 16 * QM_NT;    // columns per chunk and block in the x metadata
+constexpr int QM_META_XS = QM_MAX_BLOCKS / QM_CHB * QM_COLS;  // block sums follow the chunk scales
 constexpr uint32_t QM_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
 
 // x in fp16 planes, written by k_qmm_xprep and read by k_qmm on the same stream.
-// A operands: [block][plane hi, lo][lane 0..63] 16 bytes each. Meta: 2^-s per
-// (chunk, column) (f32, NaN for a chunk with a non-finite value) at [chunk * 16 + j],
-// then the block sums of x' = x * 2^s at [QM_META_XS + block * 16 + j] (read for
+// A operands: [column tile u][block][plane hi, lo][lane 0..63] 16 bytes each
+// (tile u holds columns 16u .. 16u + 15). Meta: 2^-s per (chunk, column j) (f32,
+// NaN for a chunk with a non-finite value) at [chunk * QM_COLS + j], then the
+// block sums of x' = x * 2^s at [QM_META_XS + block * QM_COLS + j] (read for
 // Q4_1/Q5_1). Calls that overlap on one GPU race.
-__device__ __attribute__((aligned(256))) uint4 g_qm_a[QM_MAX_BLOCKS * 2 * 64];
-__device__ __attribute__((aligned(256))) float g_qm_meta[QM_META_XS + QM_MAX_BLOCKS * 16];
+__device__ __attribute__((aligned(256))) uint4 g_qm_a[QM_NT * QM_MAX_BLOCKS * 2 * 64];
+__device__ __attribute__((aligned(256))) float g_qm_meta[QM_META_XS + QM_MAX_BLOCKS * QM_COLS];
 
 template <int TYPE>
 constexpr bool rotated_even() {
     return TYPE == TRC_HIP_TYPE_Q4_0 || TYPE == TRC_HIP_TYPE_Q5_0 || TYPE == TRC_HIP_TYPE_Q8_0;
 }
 
-// One wave per (chunk of QM_CHB blocks, column j): lane l carries block
+// One wave per (chunk of QM_CHB blocks, column j < ncol = 16 or 32): lane l carries block
 // b = l / 4 of the chunk and lane group g = l % 4. It loads exactly the 8
 // elements of A entry (b, g) (the low elements e_p and e_p + 16), the wave's
 // largest |x| and finiteness give the chunk's scale 2^s, and the lane writes its
@@ -93,11 +98,11 @@ constexpr bool rotated_even() {
 // the wave also clears its share of column j of y: rows
 // [ch * per, (ch + 1) * per) with per = ceil(M / chunks).
 __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot,
-                                                   float* __restrict__ y0, int64_t ldy, int64_t M) {
-    const int ch = blockIdx.x >> 4, j = blockIdx.x & 15;  // columns past N get zeros
+                                                   int ncol, float* __restrict__ y0, int64_t ldy, int64_t M) {
+    const int ch = blockIdx.x / ncol, j = blockIdx.x % ncol;  // columns past N get zeros
     const int l = threadIdx.x, bl = l >> 2, g = l & 3;
     if (y0 != nullptr && j < N) {
-        const int64_t nchunks = gridDim.x >> 4, per = (M + nchunks - 1) / nchunks;
+        const int64_t nchunks = gridDim.x / ncol, per = (M + nchunks - 1) / nchunks;
         const int64_t a = ch * per, e = a + per < M ? a + per : M;
         for (int64_t m = a + l; m < e; m += 64) y0[j * ldy + m] = 0.f;
     }
@@ -137,12 +142,12 @@ __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, i
     sm += __shfl_xor(sm, 1, 64);
     sm += __shfl_xor(sm, 2, 64);
     if (b < nblk) {
-        uint4* dst = g_qm_a + (int64_t) b * 2 * 64 + j + 16 * g;
+        uint4* dst = g_qm_a + ((int64_t) (j >> 4) * QM_MAX_BLOCKS + b) * 2 * 64 + (j & 15) + 16 * g;
         dst[0] = __builtin_bit_cast(uint4, hi);
         dst[64] = __builtin_bit_cast(uint4, lo);
-        if (g == 0) g_qm_meta[QM_META_XS + b * 16 + j] = sm;
+        if (g == 0) g_qm_meta[QM_META_XS + b * QM_COLS + j] = sm;
     }
-    if (l == 0) g_qm_meta[ch * 16 + j] = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
+    if (l == 0) g_qm_meta[ch * QM_COLS + j] = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
 }
 
 // Per format: which dwords of a pair each lane loads (NW of them), in bytes
@@ -298,36 +303,45 @@ constexpr int QM_CP = 8;       // pairs per K chunk (one per wave)
 static_assert(2 * QM_CP == QM_CHB, "the x scales follow the K chunks");
 constexpr int QM_RING = 3;     // chunks in flight: registers -> LDS ring depth
 
-// The x operands of one pair (two blocks) for this lane.
-struct QmX {
+// The x operands of one pair (two blocks) of one column tile for this lane.
+struct QmXT {
     h8 a[2][2];  // [block][plane hi, lo]
     f4 sc;       // 2^-s of the pair's chunk for the lane's 4 columns
     f4 xs[2];    // block sums of x' for the lane's 4 columns (Q4_1/Q5_1)
 };
+template <int NT>
+struct QmX {
+    QmXT u[NT];  // column tiles
+};
 
-template <int TYPE>
-__device__ __forceinline__ void qm_load_x(QmX& x, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rm, uint32_t ao,
-                                          uint32_t mo, int p) {
+template <int TYPE, int NT>
+__device__ __forceinline__ void qm_load_x(QmX<NT>& x, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rm,
+                                          uint32_t ao, uint32_t mo, int p) {
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int b = 2 * p + h;
+    for (int u = 0; u < NT; ++u) {
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl) {
-            x.a[h][pl] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(ra, ao, (b * 2 + pl) * 1024, 0));
+        for (int h = 0; h < 2; ++h) {
+            const int b = 2 * p + h;
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) {
+                x.u[u].a[h][pl] = __builtin_bit_cast(
+                    h8, __builtin_amdgcn_raw_buffer_load_b128(ra, ao, ((u * QM_MAX_BLOCKS + b) * 2 + pl) * 1024, 0));
+            }
+            if constexpr (MIN) {
+                x.u[u].xs[h] = __builtin_bit_cast(
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, (QM_META_XS + b * QM_COLS + 16 * u) * 4, 0));
+            }
         }
-        if constexpr (MIN) {
-            x.xs[h] = __builtin_bit_cast(
-                f4, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, (QM_META_XS + b * 16) * 4, 0));
-        }
+        x.u[u].sc = __builtin_bit_cast(
+            f4, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, ((2 * p / QM_CHB) * QM_COLS + 16 * u) * 4, 0));
     }
-    x.sc = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rm, mo, (2 * p / QM_CHB) * 64, 0));
 }
 
 // The scaled sums of one tile's pair: per block d * sum_e (q_e - BIAS) x'_e (+ m *
 // sum_e x'_e for Q4_1/Q5_1) in units of x' = x * 2^s, then back to units of x.
 template <int TYPE>
-__device__ __forceinline__ void qm_scale(const f4 (&c)[2], const uint32_t (&dm)[2], const QmX& x, f4& acc) {
+__device__ __forceinline__ void qm_scale(const f4 (&c)[2], const uint32_t (&dm)[2], const QmXT& x, f4& acc) {
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
     f4 part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -353,14 +367,16 @@ __device__ __forceinline__ void qm_scale(const f4 (&c)[2], const uint32_t (&dm)[
     }
 }
 
-// One pair of all T tiles: quant dwords from the LDS chunk, x from registers.
-// Software-pipelined over the tiles: every quant dword is read first, then
-// step t issues tile t's four MFMAs and, while they run, decodes tile t + 1
-// and scales tile t - 1, whose MFMA results are one step old. The scheduling
-// barriers keep the compiler from folding the steps back into a dependent chain.
-template <int TYPE, int T>
-__device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32_t* lo,
-                                           const QmX& x, int g, uint32_t sel, const QmK& kc, f4* acc) {
+// One pair of all T row tiles and NT column tiles: quant dwords from the LDS
+// chunk, x from registers. Each row tile's quants are decoded once for all
+// column tiles. Software-pipelined over the row tiles: every quant dword is read
+// first, then step t issues tile t's MFMAs and, while they run, decodes tile
+// t + 1 and scales tile t - 1, whose MFMA results are one step old. The
+// scheduling barriers keep the compiler from folding the steps back into a
+// dependent chain.
+template <int TYPE, int T, int NT>
+__device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32_t* lo, const QmX<NT>& x, int g,
+                                           uint32_t sel, const QmK& kc, f4 (*acc)[NT]) {
     constexpr int NW = QmFmt<TYPE>::NW, RB = QM_CP * QmFmt<TYPE>::PW * 4;  // bytes of one row in a chunk
     const f4 zero = {0.f, 0.f, 0.f, 0.f};
     uint32_t w[T][NW];
@@ -370,20 +386,30 @@ __device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32
         for (int i = 0; i < NW; ++i) w[t][i] = *(const uint32_t*) (lds_pair + lo[i] + t * 16 * (RB + 16));
     }
     QmBlocks q[T];
-    f4 c[T][2];
+    f4 c[T][NT][2];
     q[0] = qm_decode<TYPE>(w[0], g, sel, kc);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         // sum_e (q_e - BIAS) x'_e over both planes: exact products, fp32 sums
 #pragma unroll
-        for (int h = 0; h < 2; ++h) c[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.a[h][0], q[t].B[h], zero, 0, 0, 0);
+        for (int u = 0; u < NT; ++u)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) c[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.a[h][1], q[t].B[h], c[t][h], 0, 0, 0);
+            for (int h = 0; h < 2; ++h)
+                c[t][u][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.u[u].a[h][0], q[t].B[h], zero, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < NT; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                c[t][u][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.u[u].a[h][1], q[t].B[h], c[t][u][h], 0, 0, 0);
         if (t + 1 < T) q[t + 1] = qm_decode<TYPE>(w[t + 1], g, sel, kc);
-        if (t >= 1) qm_scale<TYPE>(c[t - 1], q[t - 1].dm, x, acc[t - 1]);
+        if (t >= 1) {
+#pragma unroll
+            for (int u = 0; u < NT; ++u) qm_scale<TYPE>(c[t - 1][u], q[t - 1].dm, x.u[u], acc[t - 1][u]);
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
-    qm_scale<TYPE>(c[T - 1], q[T - 1].dm, x, acc[T - 1]);
+#pragma unroll
+    for (int u = 0; u < NT; ++u) qm_scale<TYPE>(c[T - 1][u], q[T - 1].dm, x.u[u], acc[T - 1][u]);
 }
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
@@ -421,17 +447,20 @@ struct QmTile {
 // K split: blockIdx.y selects chunks [c0, c0 + part_chunks) of K. With more than
 // one part (gridDim.y == 2) the parts' sums meet in y, which k_qmm_xprep
 // cleared, by float atomic adds; 0 + a + b rounds the same in either order.
-template <int TYPE, int T, int ROUNDS, int R>
+template <int TYPE, int T, int ROUNDS, int R, int NT>
 __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict__ W, int nblk, int64_t M,
                                                         int64_t nb1_w, float* __restrict__ y, int64_t ldy, int N,
                                                         int rows_per_wg, int part_chunks) {
     using TL = QmTile<TYPE, T, ROUNDS>;
     constexpr int NW = QmFmt<TYPE>::NW, PW = TL::PW;
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
-    constexpr int NA = MIN ? 7 : 5;  // x loads per chunk and wave (two blocks x two planes, scales, block sums)
-    static_assert((R + 1) * TL::BUF >= QM_WAVES * T * 64 * 16, "reduction buffer aliases the chunk ring");
-    static_assert((R + 1) * TL::BUF <= QM_LDS, "LDS");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[(R + 1) * TL::BUF];
+    // x loads per chunk and wave: per column tile two blocks x two planes, scales, block sums
+    constexpr int NA = NT * (MIN ? 7 : 5);
+    // the chunk ring, reused at the end for the sums of every wave
+    constexpr int RED = QM_WAVES * T * NT * 64 * 16;
+    constexpr int LDS_BYTES = (R + 1) * TL::BUF > RED ? (R + 1) * TL::BUF : RED;
+    static_assert(LDS_BYTES <= QM_LDS, "LDS");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
 
     // wave index as a scalar: the pair a wave computes and its buffer offsets are wave-uniform
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -481,11 +510,13 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     const uint32_t xo = lane * 16, mo = 16 * g;
     const QmK kc = qm_consts();
 
-    f4 acc[T];
+    f4 acc[T][NT];
 #pragma unroll
-    for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int u = 0; u < NT; ++u) acc[t][u] = f4{0.f, 0.f, 0.f, 0.f};
 
-    QmX xr[R];
+    QmX<NT> xr[R];
     // W of the part's chunk c (or of its last one past the end) -> LDS buffer b
     auto load_w = [&](int c, int b) {
         const int cc = c0 + (c < nl ? c : nl - 1);
@@ -498,7 +529,7 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     // x operands of this wave's pair of the part's chunk c -> xr[xs]
     auto load_x = [&](int c, int xs) {
         const int p = (c0 + (c < nl ? c : nl - 1)) * QM_CP + wave;
-        qm_load_x<TYPE>(xr[xs], rx, rm, xo, mo, p < np ? p : np - 1);
+        qm_load_x<TYPE, NT>(xr[xs], rx, rm, xo, mo, p < np ? p : np - 1);
     };
     // Step c. Loads go out per chunk as W then x, so once at most (R - 1) chunks'
     // loads are outstanding, chunk c's W (this wave's part) and x have landed;
@@ -515,7 +546,7 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
         asm volatile("" ::: "memory");
         load_w(c + R, (c + R) % (R + 1));
         if (c < nl && (c0 + c) * QM_CP + wave < np) {
-            qm_compute<TYPE, T>(lds + (c % (R + 1)) * TL::BUF, lo, xr[xs], g, sel, kc, acc);
+            qm_compute<TYPE, T, NT>(lds + (c % (R + 1)) * TL::BUF, lo, xr[xs], g, sel, kc, acc);
         }
         load_x(c + R, xs);
     };
@@ -536,39 +567,45 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     wait_vmcnt<0>();
     __syncthreads();
 
-    // sum over the waves (fixed order) through the now idle chunk ring
+    // sum over the waves (fixed order) through the now idle chunk ring; wave
+    // w then finishes the (row tile, column tile) pairs w, w + 8, ...
     f4* red = (f4*) lds;
 #pragma unroll
-    for (int t = 0; t < T; ++t) red[(wave * T + t) * 64 + lane] = acc[t];
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int u = 0; u < NT; ++u) red[((wave * T + t) * NT + u) * 64 + lane] = acc[t][u];
     __syncthreads();
-    if (wave >= T) return;
-    const int t = wave;
-    f4 sum = red[t * 64 + lane];
+    for (int tu = wave; tu < T * NT; tu += QM_WAVES) {
+        const int t = tu % T, u = tu / T;
+        f4 sum = red[(t * NT + u) * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < QM_WAVES; ++w) sum += red[(w * T + t) * 64 + lane];
-    const int64_t m = r0 + 16 * t + m16;
-    if (m >= rend) return;
-    if (gridDim.y == 1) {
+        for (int w = 1; w < QM_WAVES; ++w) sum += red[((w * T + t) * NT + u) * 64 + lane];
+        const int64_t m = r0 + 16 * t + m16;
+        if (m >= rend) continue;
+        if (gridDim.y == 1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = 4 * g + i;
-            if (j < N) y[j * ldy + m] = sum[i];
-        }
-    } else {
+            for (int i = 0; i < 4; ++i) {
+                const int j = 16 * u + 4 * g + i;
+                if (j < N) y[j * ldy + m] = sum[i];
+            }
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = 4 * g + i;
-            if (j < N) __hip_atomic_fetch_add(y + j * ldy + m, sum[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int i = 0; i < 4; ++i) {
+                const int j = 16 * u + 4 * g + i;
+                if (j < N) {
+                    __hip_atomic_fetch_add(y + j * ldy + m, sum[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
         }
     }
 }
 
-template <int TYPE, int T, int ROUNDS, int R>
+template <int TYPE, int T, int ROUNDS, int R, int NT>
 int launch_t(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows, int parts,
              int part_chunks, hipStream_t s) {
     const int64_t grid = (M + rows - 1) / rows;
-    hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R>), dim3((unsigned) grid, (unsigned) parts), dim3(QM_WAVES * 64), 0, s,
-                       (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, y, (int64_t) (nb1_y / sizeof(float)), N, rows,
+    hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R, NT>), dim3((unsigned) grid, (unsigned) parts), dim3(QM_WAVES * 64), 0,
+                       s, (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, y, (int64_t) (nb1_y / sizeof(float)), N, rows,
                        part_chunks);
     return check_launch("qmm");
 }
@@ -585,18 +622,25 @@ constexpr int qm_buf(int t, int rounds) {
     const int fill = rounds * QM_WAVES * 64 * 16, pad = 16 * t * qm_ls16<TYPE>() * 16;
     return fill > pad ? fill : pad;
 }
-template <int TYPE>
+// With two column tiles the x register ring holds twice the operands per chunk,
+// so it is kept at 3 chunks (2 for Q4_1/Q5_1, which also carry block sums).
+template <int TYPE, int NT>
 constexpr int qm_ring(int t, int rounds) {
-    return 5 * qm_buf<TYPE>(t, rounds) <= QM_LDS ? 4 : 3;
+    constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
+    const int lds = 5 * qm_buf<TYPE>(t, rounds) <= QM_LDS ? 4 : 3;
+    const int regs = NT == 1 ? 4 : MIN ? 2 : 3;
+    return lds < regs ? lds : regs;
 }
 constexpr int qm_rounds(int rows, int ls16) {
     return (rows * ls16 + QM_WAVES * 64 - 1) / (QM_WAVES * 64);
 }
-// The most rows per workgroup (a multiple of 8, at most 112) whose ring of 4
-// buffers fits; the buffer grows with the rows, so every smaller count fits too.
-template <int TYPE>
+// The most rows per workgroup (a multiple of 8) whose ring of 4 buffers fits;
+// the buffer grows with the rows, so every smaller count fits too. At most 112
+// rows with one column tile, 64 with two (their x operands and sums double the
+// registers a row tile needs).
+template <int TYPE, int NT>
 constexpr int qm_max_rows() {
-    int r = 112;
+    int r = NT == 1 ? 112 : 64;
     while (4 * qm_buf<TYPE>((r + 15) / 16, qm_rounds(r, qm_ls16<TYPE>())) > QM_LDS) r -= 8;
     return r;
 }
@@ -604,32 +648,32 @@ constexpr int qm_max_rows() {
 // ROUNDS = 16-byte LDS pieces of a chunk per thread, rounded up. Rows come in
 // multiples of 8, so T tiles hold 16T - 8 or 16T rows and ROUNDS takes one of
 // two values.
-template <int TYPE, int T>
+template <int TYPE, int T, int NT>
 int launch_rounds(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
                   int parts, int part_chunks, hipStream_t s) {
     constexpr int LS16 = qm_ls16<TYPE>();
     constexpr int LO = qm_rounds(16 * T - 8, LS16), HI = qm_rounds(16 * T, LS16);
     const int rounds = qm_rounds(rows, LS16);
     if (rounds <= LO) {
-        return launch_t<TYPE, T, LO, qm_ring<TYPE>(T, LO)>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks,
-                                                           s);
+        return launch_t<TYPE, T, LO, qm_ring<TYPE, NT>(T, LO), NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
+                                                               part_chunks, s);
     }
-    if constexpr (16 * T <= qm_max_rows<TYPE>()) {  // 16T rows is within the cap
-        return launch_t<TYPE, T, HI, qm_ring<TYPE>(T, HI)>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks,
-                                                           s);
+    if constexpr (16 * T <= qm_max_rows<TYPE, NT>()) {  // 16T rows is within the cap
+        return launch_t<TYPE, T, HI, qm_ring<TYPE, NT>(T, HI), NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
+                                                               part_chunks, s);
     } else {
         return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
     }
 }
 
-template <int TYPE, int T>
+template <int TYPE, int T, int NT>
 int launch_tiles(int t, const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
                  int parts, int part_chunks, hipStream_t s) {
-    if constexpr (T > (qm_max_rows<TYPE>() + 15) / 16) {
+    if constexpr (T > (qm_max_rows<TYPE, NT>() + 15) / 16) {
         return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
     } else {
-        if (t == T) return launch_rounds<TYPE, T>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, s);
-        return launch_tiles<TYPE, T + 1>(t, wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, s);
+        if (t == T) return launch_rounds<TYPE, T, NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, s);
+        return launch_tiles<TYPE, T + 1, NT>(t, wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, s);
     }
 }
 
@@ -640,7 +684,7 @@ int launch_tiles(int t, const void* wq, int nblk, int64_t M, size_t nb1_w, float
 struct QmPlan {
     int rows, parts, part_chunks;
 };
-template <int TYPE>
+template <int TYPE, int NT>
 QmPlan qm_plan(int nblk, int64_t M) {
     const int nch = (nblk / 2 + QM_CP - 1) / QM_CP;
     const int64_t cus = device_cus();
@@ -650,23 +694,31 @@ QmPlan qm_plan(int nblk, int64_t M) {
     p.parts = (nch + p.part_chunks - 1) / p.part_chunks;
     int64_t rows = (M * p.parts + cus - 1) / cus;
     rows = (rows + 7) / 8 * 8;
-    if (rows > qm_max_rows<TYPE>()) rows = qm_max_rows<TYPE>();
+    if (rows > qm_max_rows<TYPE, NT>()) rows = qm_max_rows<TYPE, NT>();
     p.rows = (int) rows;
     return p;
 }
 
-template <int TYPE>
+// NT = 1 for N <= 16, 2 for 17 <= N <= 32: every column tile shares one pass over W.
+template <int TYPE, int NT>
 int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
                size_t nb1_y, hipStream_t s) {
-    const QmPlan p = qm_plan<TYPE>(nblk, M);
+    const QmPlan p = qm_plan<TYPE, NT>(nblk, M);
     const int nchunks = (nblk + QM_CHB - 1) / QM_CHB;
-    hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) (nchunks * 16)), dim3(64), 0, s, x, (int64_t) (nb1_x / sizeof(float)),
-                       N, nblk, rotated_even<TYPE>() ? 2 : 0, p.parts > 1 ? y : nullptr,
-                       (int64_t) (nb1_y / sizeof(float)), M);
+    hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) (nchunks * 16 * NT)), dim3(64), 0, s, x,
+                       (int64_t) (nb1_x / sizeof(float)), N, nblk, rotated_even<TYPE>() ? 2 : 0, 16 * NT,
+                       p.parts > 1 ? y : nullptr, (int64_t) (nb1_y / sizeof(float)), M);
     const int rc = check_launch("qmm_xprep");
     if (rc != TRC_HIP_OK) return rc;
-    return launch_tiles<TYPE, 1>((p.rows + 15) / 16, wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts, p.part_chunks,
-                                 s);
+    return launch_tiles<TYPE, 1, NT>((p.rows + 15) / 16, wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts,
+                                     p.part_chunks, s);
+}
+
+template <int TYPE>
+int launch_cols(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
+                size_t nb1_y, hipStream_t s) {
+    if (N > 16) return launch_fmt<TYPE, 2>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, s);
+    return launch_fmt<TYPE, 1>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, s);
 }
 
 }  // namespace
@@ -674,8 +726,9 @@ int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x
 bool qmm_supported(int64_t K, int64_t N, const void* wq, size_t nb1_w) {
     const int64_t nblk = K / QK;
     // K chunks are copied in 16-byte pieces (a multiple of 4 pairs per row keeps them
-    // aligned); a workgroup's 64 rows are addressed through one buffer resource (< 2^31 bytes)
-    return N >= 2 && N <= 16 && nblk >= 8 && nblk % 8 == 0 && nblk <= QM_MAX_BLOCKS &&
+    // aligned); a workgroup's rows (at most 112) are addressed through one buffer
+    // resource (< 2^31 bytes)
+    return N >= 2 && N <= 16 * QM_NT && nblk >= 8 && nblk % 8 == 0 && nblk <= QM_MAX_BLOCKS &&
            (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0 && nb1_w <= ((size_t) 1 << 24);
 }
 
@@ -683,11 +736,11 @@ int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, con
                size_t nb1_x, float* y, size_t nb1_y, hipStream_t s) {
     const int nblk = (int) (K / QK);
     switch (type) {
-        case TRC_HIP_TYPE_Q4_0: return launch_fmt<TRC_HIP_TYPE_Q4_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
-        case TRC_HIP_TYPE_Q4_1: return launch_fmt<TRC_HIP_TYPE_Q4_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
-        case TRC_HIP_TYPE_Q5_0: return launch_fmt<TRC_HIP_TYPE_Q5_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
-        case TRC_HIP_TYPE_Q5_1: return launch_fmt<TRC_HIP_TYPE_Q5_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
-        case TRC_HIP_TYPE_Q8_0: return launch_fmt<TRC_HIP_TYPE_Q8_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
+        case TRC_HIP_TYPE_Q4_0: return launch_cols<TRC_HIP_TYPE_Q4_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
+        case TRC_HIP_TYPE_Q4_1: return launch_cols<TRC_HIP_TYPE_Q4_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
+        case TRC_HIP_TYPE_Q5_0: return launch_cols<TRC_HIP_TYPE_Q5_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
+        case TRC_HIP_TYPE_Q5_1: return launch_cols<TRC_HIP_TYPE_Q5_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
+        case TRC_HIP_TYPE_Q8_0: return launch_cols<TRC_HIP_TYPE_Q8_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
         default: return fail(TRC_HIP_E_INVALID, "qmm: bad type %d", type);
     }
 }
