@@ -143,14 +143,17 @@ bool mm_shapes_ok(const int64_t a_ne[4], const int64_t b_ne[4], const int64_t d_
            d_ne[0] == a_ne[1] && d_ne[1] == b_ne[1] && d_ne[2] == b_ne[2] && d_ne[3] == b_ne[3];
 }
 
-void mm_columns(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
+void mm_outputs(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
                 const void* b, const int64_t b_ne[4], const size_t b_nb[4],
                 void* d, const size_t d_nb[4], int64_t j_begin, int64_t j_end,
-                int64_t c0, int64_t c1) {
-    // c enumerates (i3, i2, jj) with jj in [0, j_end - j_begin) fastest.
+                int64_t o0, int64_t o1) {
+    // o enumerates the outputs (i3, i2, jj, i) with i fastest, then jj in
+    // [0, j_end - j_begin). Each output is one sequential k-sum, so any split of
+    // the range over threads gives the same bits.
     const int64_t K = a_ne[0], M = a_ne[1];
     const int64_t nj = j_end - j_begin;
-    for (int64_t c = c0; c < c1; ++c) {
+    for (int64_t o = o0; o < o1; ++o) {
+        const int64_t i = o % M, c = o / M;
         const int64_t jj = c % nj;
         const int64_t i2 = (c / nj) % b_ne[2];
         const int64_t i3 = c / (nj * b_ne[2]);
@@ -158,15 +161,13 @@ void mm_columns(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
         const size_t oa = (size_t) (i2 % a_ne[2]) * a_nb[2] + (size_t) (i3 % a_ne[3]) * a_nb[3];
         const size_t ob = (size_t) i2 * b_nb[2] + (size_t) i3 * b_nb[3] + (size_t) j * b_nb[1];
         const size_t od = (size_t) i2 * d_nb[2] + (size_t) i3 * d_nb[3] + (size_t) j * d_nb[1];
-        for (int64_t i = 0; i < M; ++i) {
-            const size_t oai = oa + (size_t) i * a_nb[1];
-            float acc = 0.0f;
-            for (int64_t k = 0; k < K; ++k) {
-                const float p = ld(a, oai + (size_t) k * a_nb[0]) * ld(b, ob + (size_t) k * b_nb[0]);
-                acc = acc + p;
-            }
-            std::memcpy((uint8_t*) d + od + (size_t) i * d_nb[0], &acc, 4);
+        const size_t oai = oa + (size_t) i * a_nb[1];
+        float acc = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            const float p = ld(a, oai + (size_t) k * a_nb[0]) * ld(b, ob + (size_t) k * b_nb[0]);
+            acc = acc + p;
         }
+        std::memcpy((uint8_t*) d + od + (size_t) i * d_nb[0], &acc, 4);
     }
 }
 
@@ -250,9 +251,9 @@ int orc_mul_mat_cols(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
                      int64_t j_begin, int64_t j_end, int threads) {
     if (!mm_shapes_ok(a_ne, b_ne, d_ne)) return -1;
     if (j_begin < 0 || j_end > b_ne[1] || j_begin >= j_end) return -1;
-    const int64_t ncols = (j_end - j_begin) * b_ne[2] * b_ne[3];
-    parallel_ranges(ncols, threads, [&](int64_t c0, int64_t c1) {
-        mm_columns(a, a_ne, a_nb, b, b_ne, b_nb, d, d_nb, j_begin, j_end, c0, c1);
+    const int64_t nout = (j_end - j_begin) * b_ne[2] * b_ne[3] * a_ne[1];
+    parallel_ranges(nout, threads, [&](int64_t o0, int64_t o1) {
+        mm_outputs(a, a_ne, a_nb, b, b_ne, b_nb, d, d_nb, j_begin, j_end, o0, o1);
     });
     return 0;
 }

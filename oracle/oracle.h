@@ -72,7 +72,8 @@ int orc_dequant(int type, const void* blocks, int64_t n_blocks, float* out, int 
 /* ggml mul_mat on byte-strided F32 operands:
  *   d[i,j,i2,i3] = sum_k a[k,i,i2%a2,i3%a3] * b[k,j,i2,i3]
  * ne/nb are ggml order (ne0 innermost, nb in bytes). threads > 1 splits the
- * (i3,i2,j) output columns; each output keeps the serial k order. Returns 0, or
+ * outputs (rows i of every (i3,i2,j) column) into ranges; each output keeps the
+ * serial k order, so the bits do not depend on the thread count. Returns 0, or
  * -1 when the shapes are not a valid mul_mat. */
 int orc_mul_mat(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
                 const void* b, const int64_t b_ne[4], const size_t b_nb[4],

@@ -146,3 +146,14 @@ def test_bitwise_vs_reference_library(case):
         return np.transpose(x, np_axes)
     got = O.mul_mat(view(A, pa), view(B, pb), threads=3)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_threads_split_rows_without_changing_bits():
+    """A single output column (the matvec shape) is split over output rows when
+    threads > 1; every output keeps its serial k order, so the bits match."""
+    rng = np.random.default_rng(71)
+    A = rng.standard_normal((1, 1, 301, 257)).astype(np.float32)   # ggml [257, 301]
+    B = rng.standard_normal((1, 1, 1, 257)).astype(np.float32)     # ggml [257, 1]
+    one = O.mul_mat(A, B, threads=1)
+    for t in (2, 7, 16):
+        assert np.array_equal(O.mul_mat(A, B, threads=t).view(np.uint32), one.view(np.uint32))
