@@ -47,10 +47,10 @@
 // walks K in chunks of 8 pairs. Each chunk is copied by the whole workgroup
 // with coalesced 16-byte buffer loads straight into LDS (loads landing in MFMA
 // layout directly would touch 16 rows per instruction and swamp the L1 with
-// tag lookups), 3 or 4 chunks ahead, into a ring of R + 1 buffers whose rows
+// tag lookups), 2 to 4 chunks ahead, into a ring of R + 1 buffers whose rows
 // are padded to an odd number of 16-byte pieces (conflict-free reads); wave w
-// computes pair w of the chunk for all T tiles, so its x operands are loaded
-// once per chunk and reused over the tiles. The partial sums are added across
+// computes pair w of the chunk for all T row tiles and NT column tiles, so its
+// x operands are loaded once per chunk and reused over the row tiles. The partial sums are added across
 // the waves through LDS in a fixed order, so results are deterministic. Rows
 // per workgroup are chosen so the grid covers every CU once when M allows;
 // below 8 rows per CU, K is split in two parts whose sums meet in y by float
@@ -301,7 +301,6 @@ __device__ __forceinline__ QmBlocks qm_decode(const uint32_t* w, int g, uint32_t
 
 constexpr int QM_CP = 8;       // pairs per K chunk (one per wave)
 static_assert(2 * QM_CP == QM_CHB, "the x scales follow the K chunks");
-constexpr int QM_RING = 3;     // chunks in flight: registers -> LDS ring depth
 
 // The x operands of one pair (two blocks) of one column tile for this lane.
 struct QmXT {
