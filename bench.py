@@ -260,6 +260,8 @@ def cpu_baseline(blk: np.ndarray, x: np.ndarray, K: int, M: int, budget_s: float
     ane, anb = [K, M, 1, 1], [4, 4 * K, 4 * K * M, 4 * K * M]
     bne, bnb = [K, 1, 1, 1], [4, 4 * K, 4 * K, 4 * K]
     dne, dnb = [M, 1, 1, 1], [4, 4 * M, 4 * M, 4 * M]
+    # one untimed pass first: it touches the output pages
+    assert lib.orc_dequant(2, blk.ctypes.data, K * M // 32, wf.ctypes.data, threads) == 0
     reps, t0 = 0, time.perf_counter()
     while True:
         assert lib.orc_dequant(2, blk.ctypes.data, K * M // 32, wf.ctypes.data, threads) == 0
@@ -274,6 +276,53 @@ def cpu_baseline(blk: np.ndarray, x: np.ndarray, K: int, M: int, budget_s: float
             "sample": f"full headline workload (Q4_0 W[4096,14336] dequant to F32 + mul_mat with x[4096,1]), "
                       f"{reps} repetitions, {dt * 1e3:.1f} ms each, oracle/oracle.cpp -O3 -ffp-contract=off, "
                       f"{threads} thread{'s' if threads > 1 else ''}"}
+
+
+def cpu_other_paths(synth, budget_s: float, threads: int):
+    """The reference CPU path of the other two hot paths on this host, one thread
+    and `threads` threads (same bits): H1 = gguf_tensor_to_f32's quant branch on
+    configuration 1's Q4_0 blocks, in memory; H3 = configuration 3's forward
+    product on a bounded slice of 8 of its 512 output columns (1/64), extrapolated
+    to the whole product."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+    lib = O.oracle()
+    out = {}
+
+    def timed(fn):
+        fn()  # untimed: first touch of the output pages
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            if time.perf_counter() - t0 >= budget_s:
+                return (time.perf_counter() - t0) / reps, reps
+
+    n = 4096 * 11008 // 32
+    blk = synth.block_bytes(synth.quant_blocks(2, n, synth.config_seed(1, 2)))
+    wf = np.empty(n * 32, dtype=np.float32)
+    for nt in sorted({1, threads}):
+        dt, reps = timed(lambda nt=nt: lib.orc_dequant(2, blk.ctypes.data, n, wf.ctypes.data, nt))
+        out[f"dequant_cfg1_q4_0_{nt}t"] = {"GB/s": (blk.nbytes + n * 128) / dt / 1e9, "ms": dt * 1e3,
+                                           "threads": nt, "reps": reps}
+    del wf
+    K = M = 4096
+    T, cols = 512, 8
+    W = synth.normal(synth.config_seed(3, 0), K * M)
+    X = synth.normal(synth.config_seed(3, 1), K * T)
+    Y = np.empty(M * T, dtype=np.float32)
+    ane, anb = [K, M, 1, 1], [4, 4 * K, 4 * K * M, 4 * K * M]
+    bne, bnb = [K, T, 1, 1], [4, 4 * K, 4 * K * T, 4 * K * T]
+    dne, dnb = [M, T, 1, 1], [4, 4 * M, 4 * M * T, 4 * M * T]
+    for nt in sorted({1, threads}):
+        dt, reps = timed(lambda nt=nt: lib.orc_mul_mat_cols(W.ctypes.data, O.NE(*ane), O.NB(*anb), X.ctypes.data,
+                                                            O.NE(*bne), O.NB(*bnb), Y.ctypes.data, O.NE(*dne),
+                                                            O.NB(*dnb), 0, cols, nt))
+        fl = 2.0 * K * M * cols
+        out[f"mul_mat_cfg3_fwd_{nt}t"] = {"TFLOP/s": fl / dt / 1e12, "ms_slice": dt * 1e3,
+                                          "ms_whole_product_extrapolated": dt * 1e3 * T / cols, "threads": nt,
+                                          "reps": reps, "sample": f"{cols} of {T} output columns"}
+    return out
 
 
 def read_traffic():
@@ -383,6 +432,7 @@ def main():
         # the same path on the host's cores (a GPU box's share is 16), outputs split over threads
         nt = max(1, min(16, os.cpu_count() or 1))
         extra["cpu_baseline_all_cores"] = cpu_baseline(blk, x, K, M, args.cpu_budget / 4, nt)
+        extra["cpu_other_paths"] = cpu_other_paths(synth, args.cpu_budget / 5, nt)
 
     line = {
         "metric": METRIC,
