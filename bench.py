@@ -363,10 +363,10 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time a 256 MiB device copy (reference for the traffic counters)")
-    ap.add_argument("--only", choices=["dequant", "mul_mat", "qmm"],
+    ap.add_argument("--only", choices=["dequant", "mul_mat", "qmm", "qmm_sweep"],
                     help="only time one hot path and print its figures (for counter runs): dequant = the five "
                          "formats on configuration 1, mul_mat = configurations 3 and 4, qmm = Q4_0 N=16 on "
-                         "configuration 2")
+                         "configuration 2, qmm_sweep = Q4_0 on configuration 2 for N from 1 to 64")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; multi-GPU runs are not part of this "
@@ -391,8 +391,13 @@ def main():
         elif args.only == "mul_mat":
             part["cfg3"] = mul_mat_config3(H, synth, timer, args.steps, args.warmup)
             part["cfg4"] = mul_mat_config4(H, synth, timer, args.steps, args.warmup)
-        else:
+        elif args.only == "qmm":
             part["q4_0 N=16"], _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 16, args.steps, args.warmup)
+        else:
+            for n in (1, 2, 3, 4, 8, 12, 16, 17, 24, 32, 33, 48, 64):
+                r, _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, n, args.steps, args.warmup)
+                part[f"q4_0 N={n}"] = {"us": round(r["ms"] * 1e3, 2), "frac_hbm": round(r["frac_hbm"], 4),
+                                       "TFLOP/s": round(r["TFLOP/s"], 2)}
         print(json.dumps(part), flush=True)
         return
 
