@@ -47,7 +47,7 @@
 // walks K in chunks of 8 pairs. Each chunk is copied by the whole workgroup
 // with coalesced 16-byte buffer loads straight into LDS (loads landing in MFMA
 // layout directly would touch 16 rows per instruction and swamp the L1 with
-// tag lookups), 2 to 4 chunks ahead, into a ring of R + 1 buffers whose rows
+// tag lookups), 1 or 2 chunks ahead, into a ring of R + 1 buffers whose rows
 // are padded to an odd number of 16-byte pieces (conflict-free reads); wave w
 // computes pair w of the chunk for all T row tiles and NT column tiles, so its
 // x operands are loaded once per chunk and reused over the row tiles. The partial sums are added across
@@ -615,20 +615,20 @@ constexpr int qm_ls16() {
     return QM_CP * QmFmt<TYPE>::PW * 4 / 16 + 1;
 }
 // One chunk buffer (QmTile's BUF) for T tiles and ROUNDS pieces per thread, and
-// the ring depth R it allows: R + 1 buffers within the LDS, R = 4 or 3.
+// the ring depth R: chunks copied ahead of the one being computed.
 template <int TYPE>
 constexpr int qm_buf(int t, int rounds) {
     const int fill = rounds * QM_WAVES * 64 * 16, pad = 16 * t * qm_ls16<TYPE>() * 16;
     return fill > pad ? fill : pad;
 }
-// With two column tiles the x register ring holds twice the operands per chunk,
-// so it is kept at 3 chunks (2 for Q4_1/Q5_1, which also carry block sums).
+// Measured on configuration 2 (every format, one or two column tiles): two
+// chunks ahead beats three or four by 5-15 %; more loads in flight slow the
+// weight stream more than they hide its latency. With 6 or more row tiles a
+// step's arithmetic is long enough that one chunk ahead is best. The ring of
+// R + 1 buffers always fits: qm_max_rows keeps 4 of them within the LDS.
 template <int TYPE, int NT>
 constexpr int qm_ring(int t, int rounds) {
-    constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
-    const int lds = 5 * qm_buf<TYPE>(t, rounds) <= QM_LDS ? 4 : 3;
-    const int regs = NT == 1 ? 4 : MIN ? 2 : 3;
-    return lds < regs ? lds : regs;
+    return t >= 6 ? 1 : 2;
 }
 constexpr int qm_rounds(int rows, int ls16) {
     return (rows * ls16 + QM_WAVES * 64 - 1) / (QM_WAVES * 64);
