@@ -459,13 +459,16 @@ __global__ __launch_bounds__(QV1_WAVES * 64) void k_qmatvec_n1(const uint8_t* __
 //     bound of the same order.
 //   - Each lane owns one pair of blocks of the chunk for every row its wave
 //     processes (pairs start on 4-byte boundaries for all formats). A wave
-//     handles at most QD_RMAX rows strided over all waves, with QD_PREFETCH
+//     handles at most QD_RMAX rows strided over all waves, with one or two
 //     rows of loads in flight; each row is reduced across the wave and stored
 //     as soon as its last chunk is done.
 
 constexpr int QD_CH = 128;        // blocks per chunk of K (one lane = one pair)
 constexpr int QD_RMAX = 8;        // rows per wave at most
-constexpr int QD_PREFETCH = 3;    // rows whose loads are in flight
+// Rows whose loads are in flight per wave: one for Q8_0's 34-byte blocks, two
+// for the 4- and 5-bit formats (measured: a third row in flight adds
+// 0.1-0.6 us per Q4_0..Q8_0 call at K=4096, M=14336).
+__host__ __device__ constexpr int qd_prefetch(int type) { return type == TRC_HIP_TYPE_Q8_0 ? 1 : 2; }
 constexpr int QD_PSTRIDE = 52;    // LDS dwords per pair of planes (48 + 4: conflict-free b128 reads)
 constexpr int QD_WAVES = 8;       // waves per workgroup: one x conversion serves 8 waves
 
@@ -798,7 +801,7 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
                                                      float* __restrict__ y, int64_t ldy) {
     constexpr int BYTES = block_bytes(TYPE);
     constexpr int PW = QdFmt<TYPE>::PAIR_WORDS;
-    constexpr int PF = QD_PREFETCH < RPW ? QD_PREFETCH : RPW;
+    constexpr int PF = qd_prefetch(TYPE) < RPW ? qd_prefetch(TYPE) : RPW;
     __shared__ __attribute__((aligned(16))) uint32_t planes[NC][(QD_CH / 2) * QD_PSTRIDE];
     __shared__ float scale_l[NC][QD_CH];
     __shared__ float xsum_l[NC][QD_CH];
