@@ -738,6 +738,9 @@ constexpr bool qd_nibble_path() {
 template <int TYPE>
 __device__ __forceinline__ float qd_pair(const uint32_t* w, const uint32_t* PA, const uint32_t* PB, const float* sc,
                                          const float* xs) {
+    // the two block terms are rounded and then added, whatever the compiler
+    // would otherwise fuse into a multiply-add
+#pragma clang fp contract(off)
     constexpr uint32_t FLIP = 0x88888888u;  // unsigned nibble q -> signed q - 8
     const auto* PA3 = (const uint32_t(*)[8]) PA;
     const auto* PB3 = (const uint32_t(*)[8]) PB;
@@ -793,21 +796,116 @@ __device__ __forceinline__ float wave_sum_lane63(float v) {
     return v;
 }
 
+// Weight rows through LDS (the DMA form of the kernel). A row's segment of one
+// chunk (QD_CH blocks, a multiple of 16 bytes) is copied by 16-byte loads that go
+// straight into a per-wave LDS ring (buffer_load ... lds, streaming): consecutive
+// lanes read consecutive bytes, so each cache line is read by one instruction
+// and need not stay in the caches. Each lane then reads its pair from LDS.
+constexpr uint32_t QD_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
+constexpr int QD_DMA_NT = 2;                      // cache policy bits of the copies: nt
+
+__device__ __forceinline__ void qd_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*) lds, 16, voff, 0, 0,
+                                             QD_DMA_NT);
+}
+
+// s_waitcnt immediate with vmcnt = v (bits 3:0 and 15:14), the others at their maximum.
+constexpr int qd_vmcnt(int v) { return (v & 0xF) | ((v >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// Wait until at most k rows of NI copies each are outstanding. vmcnt also counts
+// the stores issued after a row's copies, so this waits at least as long as needed.
+template <int NI>
+__device__ __forceinline__ void qd_wait_rows(int k) {
+    static_assert(2 * NI < 64, "vmcnt is 6 bits");
+    switch (k) {
+        case 0: __builtin_amdgcn_s_waitcnt(qd_vmcnt(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(qd_vmcnt(NI)); break;
+        default: __builtin_amdgcn_s_waitcnt(qd_vmcnt(2 * NI)); break;
+    }
+}
+
+// The PW dwords of a pair at LDS byte address a, read and waited for in one asm
+// block. Plain loads would make the compiler wait for every LDS copy still in
+// flight (it cannot tell the ring's slots apart); the row's own copies are
+// waited for by qd_wait_rows instead.
+typedef uint32_t qd_u2 __attribute__((ext_vector_type(2)));
+#define QD_DS2(k, o0, o1) "ds_read2_b32 %" #k ", %[a] offset0:" #o0 " offset1:" #o1 "\n\t"
+template <int PW>
+__device__ __forceinline__ void qd_lds_words(uint32_t a, uint32_t (&w)[PW]);
+template <>
+__device__ __forceinline__ void qd_lds_words<9>(uint32_t a, uint32_t (&w)[9]) {
+    qd_u2 t[4];
+    asm volatile(QD_DS2(0, 0, 1) QD_DS2(1, 2, 3) QD_DS2(2, 4, 5) QD_DS2(3, 6, 7)
+                 "ds_read_b32 %4, %[a] offset:32\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(w[8])
+                 : [a] "v"(a));
+    for (int i = 0; i < 4; ++i) { w[2 * i] = t[i].x; w[2 * i + 1] = t[i].y; }
+}
+template <>
+__device__ __forceinline__ void qd_lds_words<10>(uint32_t a, uint32_t (&w)[10]) {
+    qd_u2 t[5];
+    asm volatile(QD_DS2(0, 0, 1) QD_DS2(1, 2, 3) QD_DS2(2, 4, 5) QD_DS2(3, 6, 7) QD_DS2(4, 8, 9)
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4])
+                 : [a] "v"(a));
+    for (int i = 0; i < 5; ++i) { w[2 * i] = t[i].x; w[2 * i + 1] = t[i].y; }
+}
+template <>
+__device__ __forceinline__ void qd_lds_words<11>(uint32_t a, uint32_t (&w)[11]) {
+    qd_u2 t[5];
+    asm volatile(QD_DS2(0, 0, 1) QD_DS2(1, 2, 3) QD_DS2(2, 4, 5) QD_DS2(3, 6, 7) QD_DS2(4, 8, 9)
+                 "ds_read_b32 %5, %[a] offset:40\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(w[10])
+                 : [a] "v"(a));
+    for (int i = 0; i < 5; ++i) { w[2 * i] = t[i].x; w[2 * i + 1] = t[i].y; }
+}
+template <>
+__device__ __forceinline__ void qd_lds_words<12>(uint32_t a, uint32_t (&w)[12]) {
+    qd_u2 t[6];
+    asm volatile(QD_DS2(0, 0, 1) QD_DS2(1, 2, 3) QD_DS2(2, 4, 5) QD_DS2(3, 6, 7) QD_DS2(4, 8, 9) QD_DS2(5, 10, 11)
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5])
+                 : [a] "v"(a));
+    for (int i = 0; i < 6; ++i) { w[2 * i] = t[i].x; w[2 * i + 1] = t[i].y; }
+}
+template <>
+__device__ __forceinline__ void qd_lds_words<17>(uint32_t a, uint32_t (&w)[17]) {
+    qd_u2 t[8];
+    asm volatile(QD_DS2(0, 0, 1) QD_DS2(1, 2, 3) QD_DS2(2, 4, 5) QD_DS2(3, 6, 7) QD_DS2(4, 8, 9) QD_DS2(5, 10, 11)
+                     QD_DS2(6, 12, 13) QD_DS2(7, 14, 15) "ds_read_b32 %8, %[a] offset:64\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]),
+                   "=&v"(t[7]), "=&v"(w[16])
+                 : [a] "v"(a));
+    for (int i = 0; i < 8; ++i) { w[2 * i] = t[i].x; w[2 * i + 1] = t[i].y; }
+}
+#undef QD_DS2
+
+// Workgroup barrier after this wave's LDS writes are done. __syncthreads' fence
+// would also wait for every LDS copy in flight, which drains the weight stream.
+__device__ __forceinline__ void qd_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // NC columns of x (1 or 2) share one pass over W: each row's quant words are
 // decoded once and met by every column's digit planes (48 registers per column).
-template <int TYPE, int RPW, int NC>
+// DMA: weight rows through LDS (needs 16-byte aligned rows and nblk % 8 == 0);
+// otherwise each lane loads its pair into registers.
+template <int TYPE, int RPW, int NC, bool DMA>
 __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __restrict__ W, int64_t nblk, int64_t M,
                                                      int64_t nb1_w, const float* __restrict__ x, int64_t ldx,
                                                      float* __restrict__ y, int64_t ldy) {
     constexpr int BYTES = block_bytes(TYPE);
     constexpr int PW = QdFmt<TYPE>::PAIR_WORDS;
     constexpr int PF = qd_prefetch(TYPE) < RPW ? qd_prefetch(TYPE) : RPW;
+    constexpr int SEG = QD_CH * BYTES;        // bytes of a row's full chunk
+    constexpr int NI = (SEG + 1023) / 1024;   // 16-byte copies per lane and row
+    constexpr int SLOTS = PF + 1;             // rows in flight + the row being read
+    __shared__ __attribute__((aligned(16))) uint8_t wring[DMA ? QD_WAVES : 1][DMA ? SLOTS : 1][DMA ? NI * 1024 : 16];
     __shared__ __attribute__((aligned(16))) uint32_t planes[NC][(QD_CH / 2) * QD_PSTRIDE];
     __shared__ float scale_l[NC][QD_CH];
     __shared__ float xsum_l[NC][QD_CH];
 
     const int lane = threadIdx.x & 63;
-    const int64_t wave_id = (int64_t) blockIdx.x * QD_WAVES + (threadIdx.x >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t wave_id = (int64_t) blockIdx.x * QD_WAVES + wv;
     // Rows are strided over the waves (row = wave + r * n_waves), so the loads
     // in flight at any time sweep W in address order rather than starting in
     // every wave's own region.
@@ -831,16 +929,38 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         for (int r = 0; r < RPW; ++r) acc[n][r] = 0.f;
 
     const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
-    uint32_t w[RPW][PW];
+    uint32_t w[DMA ? 1 : RPW][PW];
     for (int64_t c = 0; c < nchunks; ++c) {
         const int64_t cb = nblk - c * QD_CH < QD_CH ? nblk - c * QD_CH : QD_CH;
         const bool mine = 2 * lane < cb;  // this lane owns a pair of this chunk (cb is even)
         const int pl = mine ? lane : (int) (cb / 2) - 1;
         const uint8_t* base = W + (c * QD_CH + 2 * pl) * BYTES;
+        // Prefetching stays within a chunk, so row r of every chunk can use ring
+        // slot r % SLOTS: the slot's previous row was read (and waited for) before.
         auto issue = [&](int r) {
-            const uint32_t* p32 = (const uint32_t*) (base + roff[r]);
+            if constexpr (DMA) {
+                // lanes past a short last chunk read zeros (the buffer's range check)
+                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                    (void*) (W + roff[r] + c * (int64_t) SEG), (short) 0, (int) cb * BYTES, QD_RSRC_WORD3);
 #pragma unroll
-            for (int i = 0; i < PW; ++i) w[r][i] = p32[i];
+                for (int i = 0; i < NI; ++i) qd_dma16(rs, &wring[wv][r % SLOTS][i * 1024], (uint32_t) (i * 1024 + 16 * lane));
+            } else {
+                const uint32_t* p32 = (const uint32_t*) (base + roff[r]);
+#pragma unroll
+                for (int i = 0; i < PW; ++i) w[r][i] = p32[i];
+            }
+        };
+        // this lane's pair of row r, in registers
+        auto pair_words = [&](int r) -> const uint32_t* {
+            if constexpr (DMA) {
+                qd_wait_rows<NI>(RPW - 1 - r < PF ? RPW - 1 - r : PF);
+                const uint32_t a = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t*) &wring[wv][r % SLOTS][0] +
+                                   (uint32_t) pl * (PW * 4);
+                qd_lds_words<PW>(a, w[0]);
+                return w[0];
+            } else {
+                return w[r];
+            }
         };
         // x is loaded first (vector loads return in issue order), then the
         // weight stream starts so that it overlaps the conversion of x
@@ -858,7 +978,7 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         for (int r = 0; r < PF; ++r) issue(r);
         // keep these loads above the prologue and its barrier
         __builtin_amdgcn_sched_barrier(0);
-        if (c > 0) __syncthreads();  // previous chunk's planes are no longer read
+        if (c > 0) qd_barrier();  // previous chunk's planes are no longer read
 #pragma unroll
         for (int n = 0; n < NC; ++n) {
             if constexpr (qd_nibble_path<TYPE>()) {
@@ -867,7 +987,7 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
                 qd_prologue<TYPE == TRC_HIP_TYPE_Q8_0>(xv[n], cb, planes[n], scale_l[n], xsum_l[n]);
             }
         }
-        __syncthreads();
+        qd_barrier();
 
         // this lane's pair: the plane words of blocks A and B (24 each) per column.
         // Nibble path: A at dwords 0-23, B at 24-47. Byte path: plane p of A at
@@ -898,9 +1018,10 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         for (int r = 0; r < RPW; ++r) {
             if (r + PF < RPW) issue(r + PF);
             __builtin_amdgcn_sched_barrier(0);  // row r + PF stays in flight during row r
+            const uint32_t* wr = pair_words(r);
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
-                const float v = qd_pair<TYPE>(w[r], PA[n], PB[n], sc[n], xs[n]);
+                const float v = qd_pair<TYPE>(wr, PA[n], PB[n], sc[n], xs[n]);
                 acc[n][r] += mine ? v : 0.f;
             }
             // after the last chunk a row is final: reduce and store it while the
@@ -924,9 +1045,17 @@ int launch_dot_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const 
                    size_t nb1_y, hipStream_t s) {
     const int64_t waves = (M + RPW - 1) / RPW;
     const int64_t grid = (waves + QD_WAVES - 1) / QD_WAVES;
-    hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s,
-                       (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, (int64_t) (nb1_x / sizeof(float)), y,
-                       (int64_t) (nb1_y / sizeof(float)));
+    // the LDS copies need 16-byte aligned row chunks (8 blocks are a multiple of 16 bytes)
+    const bool dma = nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0;
+    if (dma) {
+        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s,
+                           (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, (int64_t) (nb1_x / sizeof(float)), y,
+                           (int64_t) (nb1_y / sizeof(float)));
+    } else {
+        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, false>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s,
+                           (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, (int64_t) (nb1_x / sizeof(float)), y,
+                           (int64_t) (nb1_y / sizeof(float)));
+    }
     return check_launch("qmatvec_dot");
 }
 
