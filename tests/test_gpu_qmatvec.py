@@ -56,6 +56,30 @@ def test_config2_decode_shapes(hip, name, N):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("N", [1, 2])
+@pytest.mark.parametrize("K,M,w_off", [(32 * 130, 3001, 0), (32 * 264, 999, 4), (32 * 264, 999, 0), (512, 20000, 0)])
+def test_dot_kernel_weight_paths(hip, name, N, K, M, w_off):
+    """The one- and two-column kernel's ways of reading W: into registers (130
+    blocks per row, not a multiple of 8; or W 4 bytes off a 16-byte boundary),
+    through LDS over two full chunks of 128 blocks and a short one (264 blocks),
+    and through LDS with more workgroups than CUs (20000 rows of 8 per wave)."""
+    t = TYPES[name]
+    announce(f"qmatvec dot paths {name} N={N} K={K} M={M} w_off={w_off}")
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 1000 + K + M))
+    X = synth.normal(K + 7 * M, K * N).reshape(1, 1, N, K)
+    padded = np.zeros(raw.nbytes + w_off, np.uint8)
+    padded[w_off:] = raw
+    dw, dx = Dev(padded), Dev(X)
+    dy = empty((1, 1, N, M))
+    H.qmatvec(t, dw.ptr + w_off, K, M, (K // 32) * H.BLOCK_BYTES[t], dx.ptr, N, K * 4, dy.ptr, M * 4)
+    H.sync()
+    got = np.ascontiguousarray(dy.read())
+    for d in (dw, dx, dy):
+        d.free()
+    assert O.row_l2_error(got, oracle_qmatvec(t, raw, K, M, X)) <= TOL
+
+
+@pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("N", [1, 2, 3, 5, 8, 13, 16])
 def test_all_formats_small(hip, name, N):
     t = TYPES[name]

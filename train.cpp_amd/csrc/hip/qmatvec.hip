@@ -465,10 +465,15 @@ __global__ __launch_bounds__(QV1_WAVES * 64) void k_qmatvec_n1(const uint8_t* __
 
 constexpr int QD_CH = 128;        // blocks per chunk of K (one lane = one pair)
 constexpr int QD_RMAX = 8;        // rows per wave at most
-// Rows whose loads are in flight per wave: one for Q8_0's 34-byte blocks, two
-// for the 4- and 5-bit formats (measured: a third row in flight adds
-// 0.1-0.6 us per Q4_0..Q8_0 call at K=4096, M=14336).
-__host__ __device__ constexpr int qd_prefetch(int type) { return type == TRC_HIP_TYPE_Q8_0 ? 1 : 2; }
+// Rows whose loads are in flight per wave, as measured (K=4096, M=14336 and
+// K=14336, M=4096): two for one column of a 4- or 5-bit format (one row adds
+// 0.5 us per call, a third 0.1-0.5 us); one for Q8_0's 34-byte blocks, for two
+// columns, and when the grid takes more than one workgroup per CU (the smaller
+// LDS ring then lets two workgroups share a CU).
+constexpr int qd_prefetch(int type, int nc, bool dma, bool crowded) {
+    if (!dma) return type == TRC_HIP_TYPE_Q8_0 ? 1 : 2;
+    return crowded || nc > 1 || type == TRC_HIP_TYPE_Q8_0 ? 1 : 2;
+}
 constexpr int QD_PSTRIDE = 52;    // LDS dwords per pair of planes (48 + 4: conflict-free b128 reads)
 constexpr int QD_WAVES = 8;       // waves per workgroup: one x conversion serves 8 waves
 
@@ -888,13 +893,14 @@ __device__ __forceinline__ void qd_barrier() { asm volatile("s_waitcnt lgkmcnt(0
 // decoded once and met by every column's digit planes (48 registers per column).
 // DMA: weight rows through LDS (needs 16-byte aligned rows and nblk % 8 == 0);
 // otherwise each lane loads its pair into registers.
-template <int TYPE, int RPW, int NC, bool DMA>
+template <int TYPE, int RPW, int NC, bool DMA, int PF_ROWS>
 __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __restrict__ W, int64_t nblk, int64_t M,
                                                      int64_t nb1_w, const float* __restrict__ x, int64_t ldx,
                                                      float* __restrict__ y, int64_t ldy) {
     constexpr int BYTES = block_bytes(TYPE);
     constexpr int PW = QdFmt<TYPE>::PAIR_WORDS;
-    constexpr int PF = qd_prefetch(TYPE) < RPW ? qd_prefetch(TYPE) : RPW;
+    constexpr int PF = PF_ROWS < RPW ? PF_ROWS : RPW;
+    static_assert(RPW <= 64, "each of a wave's rows is stored by one lane");
     constexpr int SEG = QD_CH * BYTES;        // bytes of a row's full chunk
     constexpr int NI = (SEG + 1023) / 1024;   // 16-byte copies per lane and row
     constexpr int SLOTS = PF + 1;             // rows in flight + the row being read
@@ -923,10 +929,13 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
     }
 
     float acc[NC][RPW];
+    float out[NC];  // lane r: row r's result
 #pragma unroll
-    for (int n = 0; n < NC; ++n)
+    for (int n = 0; n < NC; ++n) {
+        out[n] = 0.f;
 #pragma unroll
         for (int r = 0; r < RPW; ++r) acc[n][r] = 0.f;
+    }
 
     const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
     uint32_t w[DMA ? 1 : RPW][PW];
@@ -1024,20 +1033,26 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
                 const float v = qd_pair<TYPE>(wr, PA[n], PB[n], sc[n], xs[n]);
                 acc[n][r] += mine ? v : 0.f;
             }
-            // after the last chunk a row is final: reduce and store it while the
-            // next rows' loads are in flight, so the wave ends one reduction
-            // after its last row instead of RPW
+            // after the last chunk a row is final: reduce it while the next
+            // rows' loads are in flight and keep the sum in lane r
             if (c == nchunks - 1) {
-                const int64_t row = wave_id + r * n_waves;
 #pragma unroll
                 for (int n = 0; n < NC; ++n) {
                     const float sum = wave_sum_lane63(acc[n][r]);
-                    if (lane == 63 && row < M) y[n * ldy + row] = sum;
+                    const float s63 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 63));
+                    out[n] = lane == r ? s63 : out[n];
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+    // One store per column for all of the wave's rows, after the last load: a
+    // store inside the stream holds up the in-order wait for the rows behind it
+    // (measured: 0.2 us per Q4_0 call, 0.6 us per Q8_0 call at K=4096, M=14336).
+    const int64_t row = wave_id + (int64_t) lane * n_waves;
+#pragma unroll
+    for (int n = 0; n < NC; ++n)
+        if (lane < RPW && row < M) y[n * ldy + row] = out[n];
 }
 
 template <int TYPE, int RPW, int NC>
@@ -1047,14 +1062,26 @@ int launch_dot_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const 
     const int64_t grid = (waves + QD_WAVES - 1) / QD_WAVES;
     // the LDS copies need 16-byte aligned row chunks (8 blocks are a multiple of 16 bytes)
     const bool dma = nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0;
+    const dim3 g((unsigned) grid), b(QD_WAVES * 64);
+    const int64_t ldx = (int64_t) (nb1_x / sizeof(float)), ldy = (int64_t) (nb1_y / sizeof(float));
+    const auto* w = (const uint8_t*) wq;
+    // only the largest row count per wave can leave more workgroups than CUs
+    if constexpr (RPW == QD_RMAX) {
+        if (dma && grid > device_cus()) {
+            constexpr int PF = qd_prefetch(TYPE, NC, true, true);
+            hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true, PF>), g, b, 0, s, w, nblk, M, (int64_t) nb1_w, x,
+                               ldx, y, ldy);
+            return check_launch("qmatvec_dot");
+        }
+    }
     if (dma) {
-        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s,
-                           (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, (int64_t) (nb1_x / sizeof(float)), y,
-                           (int64_t) (nb1_y / sizeof(float)));
+        constexpr int PF = qd_prefetch(TYPE, NC, true, false);
+        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true, PF>), g, b, 0, s, w, nblk, M, (int64_t) nb1_w, x, ldx,
+                           y, ldy);
     } else {
-        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, false>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s,
-                           (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, (int64_t) (nb1_x / sizeof(float)), y,
-                           (int64_t) (nb1_y / sizeof(float)));
+        constexpr int PF = qd_prefetch(TYPE, NC, false, false);
+        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, false, PF>), g, b, 0, s, w, nblk, M, (int64_t) nb1_w, x, ldx,
+                           y, ldy);
     }
     return check_launch("qmatvec_dot");
 }

@@ -422,7 +422,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane
 // (buffer_load_dwordx4 ... lds; the LDS base goes through M0).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*) lds, 16, voff, soff, 0, 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*) lds, 16, voff, soff, 0, 0);
 }
 
 template <int TYPE, int T, int ROUNDS>
