@@ -35,6 +35,22 @@ def test_roundtrip_and_fill(hip):
     assert np.all(d.read()[:2] == 0)
 
 
+@pytest.mark.parametrize("offset,count", [(0, 1003), (16, 8), (0, 3), (32, 2_000_001), (4, 5)])
+def test_fill_aligned_and_tails(hip, offset, count):
+    """16-byte aligned fills take whole float4 stores plus a tail of count % 4;
+    others go float by float. Neighbours on both sides stay untouched."""
+    x = np.arange(count + 64, dtype=np.float32)
+    d = Dev(x)
+    H.fill_f32(d.ptr + offset, 7.25, count)
+    H.sync()
+    y = d.read()
+    o = offset // 4
+    assert np.array_equal(y[:o], x[:o])
+    assert np.all(y[o:o + count] == 7.25)
+    assert np.array_equal(y[o + count:], x[o + count:])
+    d.free()
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.uint8, np.int16, np.float64])
 def test_cpy_transpose_is_cont(hip, dtype):
     announce(f"abi cpy {dtype}")

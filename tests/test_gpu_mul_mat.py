@@ -106,6 +106,9 @@ def test_backward_goldens(hip, case):
     # K, M, N, b2, b3, a2, a3
     (1, 1, 1, 1, 1, 1, 1), (2, 33, 31, 1, 1, 1, 1), (17, 65, 129, 1, 1, 1, 1), (100, 130, 70, 3, 2, 3, 1),
     (256, 256, 256, 1, 1, 1, 1), (513, 200, 300, 2, 1, 1, 1), (64, 128, 128, 4, 2, 2, 2), (7, 9, 11, 6, 1, 3, 1),
+    # 128 or more 128x128 tiles but under 512 and K >= 1024: K in two parts summed
+    # by atomic adds (partial tiles, K not a multiple of the slab, two planes)
+    (2500, 2000, 1000, 1, 1, 1, 1), (1030, 1000, 1000, 1, 1, 2, 1),
 ])
 @pytest.mark.parametrize("layout", ["kk", "tk", "kt", "tt", "gen"])
 def test_random_shapes_and_layouts(hip, shape, layout):

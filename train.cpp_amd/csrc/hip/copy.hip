@@ -15,6 +15,15 @@ __global__ __launch_bounds__(CP_THREADS) void k_fill_f32(float* __restrict__ dst
     }
 }
 
+// 16-byte stores for a 16-byte aligned dst; the last n % 4 floats go one by one.
+__global__ __launch_bounds__(CP_THREADS) void k_fill_f32x4(f4* __restrict__ dst, float value, int64_t n4,
+                                                          float* __restrict__ tail, int ntail) {
+    const f4 v = {value, value, value, value};
+    const int64_t stride = (int64_t) gridDim.x * CP_THREADS;
+    for (int64_t i = (int64_t) blockIdx.x * CP_THREADS + threadIdx.x; i < n4; i += stride) dst[i] = v;
+    if (blockIdx.x == 0 && (int) threadIdx.x < ntail) tail[threadIdx.x] = value;
+}
+
 // Copies element i of src to element i of dst in ggml linear order
 // (tensor_offset_linear, src/core/trc_tensor.cpp:95-103), ne0 fastest. The
 // launch covers ne0 x rows with x along ne0, so a run of ne0 is one wave's
@@ -45,7 +54,13 @@ unsigned grid_for(int64_t n) {
 }  // namespace
 
 int launch_fill_f32(float* dst, float value, int64_t count, hipStream_t stream) {
-    hipLaunchKernelGGL(k_fill_f32, dim3(grid_for(count)), dim3(CP_THREADS), 0, stream, dst, value, count);
+    if ((((uintptr_t) dst) & 15u) == 0) {
+        const int64_t n4 = count / 4;
+        hipLaunchKernelGGL(k_fill_f32x4, dim3(grid_for(n4)), dim3(CP_THREADS), 0, stream, (f4*) dst, value, n4,
+                           dst + 4 * n4, (int) (count - 4 * n4));
+    } else {
+        hipLaunchKernelGGL(k_fill_f32, dim3(grid_for(count)), dim3(CP_THREADS), 0, stream, dst, value, count);
+    }
     return check_launch("fill_f32");
 }
 

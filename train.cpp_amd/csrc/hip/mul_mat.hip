@@ -26,12 +26,15 @@
 //     GENERIC (scalar loads for any other stride). Out-of-range elements load 0.
 //   - The next slab is fetched into registers while the current one is being
 //     multiplied, so global latency overlaps MFMA work.
+//   - When 128x128 tiles would give under two workgroups per CU, K is split in
+//     two: 8-wave workgroups (64x32 per wave) each sum half of K for one tile,
+//     into a dst cleared beforehand, with float atomic adds. 0 + a + b rounds
+//     the same in either order, so results stay deterministic.
 #include "common.h"
 
 namespace trc_hip {
 namespace {
 
-constexpr int MM_THREADS = 256;
 
 enum LoadMode { K_CONTIG = 0, R_CONTIG = 1, GENERIC = 2 };
 
@@ -48,10 +51,10 @@ struct MMArgs {
 
 // Loads a ROWS x BK slab (rows = i for src0, j for src1) of one operand into
 // registers, then stores it to LDS as lds[k * LD + row].
-template <int MODE, int ROWS, int BK>
+template <int MODE, int ROWS, int BK, int THREADS>
 struct SlabLoader {
     static constexpr int LD = ROWS + 4;
-    static constexpr int PER = ROWS * BK / MM_THREADS;  // floats per thread
+    static constexpr int PER = ROWS * BK / THREADS;  // floats per thread
     static_assert(PER % 4 == 0, "slab must give each thread whole float4s");
     float r[PER];
 
@@ -60,7 +63,7 @@ struct SlabLoader {
         if constexpr (MODE == K_CONTIG) {
 #pragma unroll
             for (int u = 0; u < PER / 4; ++u) {
-                const int q = tid + MM_THREADS * u;
+                const int q = tid + THREADS * u;
                 const int row = q / (BK / 4);
                 const int kq = q % (BK / 4);
                 const int64_t gr = row0 + row;
@@ -75,7 +78,7 @@ struct SlabLoader {
         } else if constexpr (MODE == R_CONTIG) {
 #pragma unroll
             for (int u = 0; u < PER / 4; ++u) {
-                const int q = tid + MM_THREADS * u;
+                const int q = tid + THREADS * u;
                 const int k = q / (ROWS / 4);
                 const int rq = q % (ROWS / 4);
                 const int64_t gr = row0 + 4 * rq;
@@ -90,7 +93,7 @@ struct SlabLoader {
         } else {
 #pragma unroll
             for (int u = 0; u < PER; ++u) {
-                const int e = tid + MM_THREADS * u;
+                const int e = tid + THREADS * u;
                 const int row = e % ROWS;
                 const int k = e / ROWS;
                 const int64_t gr = row0 + row;
@@ -106,7 +109,7 @@ struct SlabLoader {
         if constexpr (MODE == K_CONTIG) {
 #pragma unroll
             for (int u = 0; u < PER / 4; ++u) {
-                const int q = tid + MM_THREADS * u;
+                const int q = tid + THREADS * u;
                 const int row = q / (BK / 4);
                 const int kq = q % (BK / 4);
 #pragma unroll
@@ -115,7 +118,7 @@ struct SlabLoader {
         } else if constexpr (MODE == R_CONTIG) {
 #pragma unroll
             for (int u = 0; u < PER / 4; ++u) {
-                const int q = tid + MM_THREADS * u;
+                const int q = tid + THREADS * u;
                 const int k = q / (ROWS / 4);
                 const int rq = q % (ROWS / 4);
                 f4 v = {r[4 * u + 0], r[4 * u + 1], r[4 * u + 2], r[4 * u + 3]};
@@ -124,20 +127,22 @@ struct SlabLoader {
         } else {
 #pragma unroll
             for (int u = 0; u < PER; ++u) {
-                const int e = tid + MM_THREADS * u;
+                const int e = tid + THREADS * u;
                 lds[(e / ROWS) * LD + (e % ROWS)] = r[u];
             }
         }
     }
 };
 
-template <int WI, int WJ, int TI, int TJ, int BK, int AMODE, int BMODE>
-__global__ __launch_bounds__(MM_THREADS) void k_mul_mat(MMArgs p) {
-    static_assert(WI * WJ * 64 == MM_THREADS, "four waves per workgroup");
+// SPLIT: parts of K (1, or 2 summed into a cleared dst with atomic adds).
+template <int WI, int WJ, int TI, int TJ, int BK, int AMODE, int BMODE, int SPLIT>
+__global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
+    constexpr int THREADS = WI * WJ * 64;
+    static_assert(SPLIT == 1 || SPLIT == 2, "two parts at most keep the atomic sums deterministic");
     constexpr int BM = WI * TI * 32;  // tile extent along i
     constexpr int BN = WJ * TJ * 32;  // tile extent along j
-    using LA = SlabLoader<AMODE, BM, BK>;
-    using LB = SlabLoader<BMODE, BN, BK>;
+    using LA = SlabLoader<AMODE, BM, BK, THREADS>;
+    using LB = SlabLoader<BMODE, BN, BK, THREADS>;
     __shared__ __attribute__((aligned(16))) float As[BK * LA::LD];
     __shared__ __attribute__((aligned(16))) float Bs[BK * LB::LD];
 
@@ -148,6 +153,8 @@ __global__ __launch_bounds__(MM_THREADS) void k_mul_mat(MMArgs p) {
     const int wj = wave / WI;
 
     int64_t t = blockIdx.x;
+    const int part = SPLIT > 1 ? (int) (t % SPLIT) : 0;
+    t /= SPLIT;
     const int64_t ti = t % p.tiles_i;
     t /= p.tiles_i;
     const int64_t tj = t % p.tiles_j;
@@ -171,9 +178,13 @@ __global__ __launch_bounds__(MM_THREADS) void k_mul_mat(MMArgs p) {
 
     LA la;
     LB lb;
-    const int64_t nk = (p.K + BK - 1) / BK;
-    la.load(a, p.a_nb0, p.a_nb1, i0, p.M, 0, p.K, tid);
-    lb.load(b, p.b_nb0, p.b_nb1, j0, p.N, 0, p.K, tid);
+    // this part's slabs: [kt0, kt0 + nk)
+    const int64_t slabs = (p.K + BK - 1) / BK;
+    const int64_t per_part = (slabs + SPLIT - 1) / SPLIT;
+    const int64_t kt0 = part * per_part;
+    const int64_t nk = slabs - kt0 < per_part ? slabs - kt0 : per_part;
+    la.load(a, p.a_nb0, p.a_nb1, i0, p.M, kt0 * BK, p.K, tid);
+    lb.load(b, p.b_nb0, p.b_nb1, j0, p.N, kt0 * BK, p.K, tid);
     la.store(As, tid);
     lb.store(Bs, tid);
     __syncthreads();
@@ -183,8 +194,8 @@ __global__ __launch_bounds__(MM_THREADS) void k_mul_mat(MMArgs p) {
     for (int64_t kt = 0; kt < nk; ++kt) {
         const bool more = kt + 1 < nk;
         if (more) {
-            la.load(a, p.a_nb0, p.a_nb1, i0, p.M, (kt + 1) * BK, p.K, tid);
-            lb.load(b, p.b_nb0, p.b_nb1, j0, p.N, (kt + 1) * BK, p.K, tid);
+            la.load(a, p.a_nb0, p.a_nb1, i0, p.M, (kt0 + kt + 1) * BK, p.K, tid);
+            lb.load(b, p.b_nb0, p.b_nb1, j0, p.N, (kt0 + kt + 1) * BK, p.K, tid);
         }
 #pragma unroll
         for (int s = 0; s < BK / 2; ++s) {
@@ -219,7 +230,13 @@ __global__ __launch_bounds__(MM_THREADS) void k_mul_mat(MMArgs p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t j = j0 + (wj * TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                if (j < p.N) *(float*) (d + i * p.d_nb0 + j * p.d_nb1) = acc[x][y][v];
+                if (j >= p.N) continue;
+                float* dst = (float*) (d + i * p.d_nb0 + j * p.d_nb1);
+                if constexpr (SPLIT > 1) {
+                    __hip_atomic_fetch_add(dst, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    *dst = acc[x][y][v];
+                }
             }
         }
     }
@@ -236,21 +253,22 @@ int pick_mode(const trc_hip_tensor& t, int64_t rows) {
     return GENERIC;
 }
 
-template <int WI, int WJ, int TI, int TJ, int BK, int AM, int BMO>
+template <int WI, int WJ, int TI, int TJ, int BK, int AM, int BMO, int SPLIT>
 int launch_cfg(MMArgs& p, int64_t planes, hipStream_t stream) {
     constexpr int BM = WI * TI * 32, BN = WJ * TJ * 32;
     p.tiles_i = (p.M + BM - 1) / BM;
     p.tiles_j = (p.N + BN - 1) / BN;
-    const int64_t grid = p.tiles_i * p.tiles_j * planes;
+    const int64_t grid = p.tiles_i * p.tiles_j * planes * SPLIT;
     if (grid > 0x7FFFFFFF) return fail(TRC_HIP_E_SHAPE, "mul_mat: %lld workgroups exceed one launch", (long long) grid);
-    hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, BK, AM, BMO>), dim3((unsigned) grid), dim3(MM_THREADS), 0, stream, p);
+    hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, BK, AM, BMO, SPLIT>), dim3((unsigned) grid), dim3(WI * WJ * 64), 0,
+                       stream, p);
     return check_launch("mul_mat_f32");
 }
 
-template <int WI, int WJ, int TI, int TJ, int BK>
+template <int WI, int WJ, int TI, int TJ, int BK, int SPLIT>
 int dispatch_modes(MMArgs& p, int am, int bm, int64_t planes, hipStream_t s) {
 #define TRC_MM_CASE(A, B) \
-    if (am == A && bm == B) return launch_cfg<WI, WJ, TI, TJ, BK, A, B>(p, planes, s);
+    if (am == A && bm == B) return launch_cfg<WI, WJ, TI, TJ, BK, A, B, SPLIT>(p, planes, s);
     TRC_MM_CASE(K_CONTIG, K_CONTIG)
     TRC_MM_CASE(K_CONTIG, R_CONTIG)
     TRC_MM_CASE(K_CONTIG, GENERIC)
@@ -284,11 +302,19 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
     const int bm = pick_mode(b, p.N);
     const int64_t planes = b.ne[2] * b.ne[3];
 
-    // Large tiles when they still give every CU at least two workgroups;
-    // otherwise 64x64 tiles to fill the chip.
+    // Large tiles when they still give every CU at least two workgroups. With
+    // between half and two tiles per CU and a long K, large tiles with K in two
+    // parts (into a cleared, contiguous dst); otherwise 64x64 tiles.
     const int64_t big_tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128) * planes;
-    if (big_tiles >= 512) return dispatch_modes<2, 2, 2, 2, 16>(p, am, bm, planes, stream);
-    return dispatch_modes<2, 2, 1, 1, 32>(p, am, bm, planes, stream);
+    if (big_tiles >= 512) return dispatch_modes<2, 2, 2, 2, 16, 1>(p, am, bm, planes, stream);
+    const bool dense_dst = p.d_nb0 == 4 && p.d_nb1 == 4 * p.M && p.d_nb2 == p.d_nb1 * p.N &&
+                           p.d_nb3 == p.d_nb2 * b.ne[2];
+    if (dense_dst && p.K >= 1024 && 2 * big_tiles >= device_cus()) {
+        const int rc = launch_fill_f32((float*) d.data, 0.f, p.M * p.N * planes, stream);
+        if (rc != TRC_HIP_OK) return rc;
+        return dispatch_modes<2, 4, 2, 1, 16, 2>(p, am, bm, planes, stream);
+    }
+    return dispatch_modes<2, 2, 1, 1, 32, 1>(p, am, bm, planes, stream);
 }
 
 }  // namespace trc_hip
