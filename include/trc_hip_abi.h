@@ -141,7 +141,9 @@ int trc_hip_dequant(int type, const void* blocks, int64_t n_blocks, float* dst, 
  * broadcast of src0. Serves OP_MUL_MAT (src/ops/trc_ops.cpp:366-385) as
  * computed by compute_mul_mat (src/backends/cpu/trc_cpu_ops.cpp:182-216).
  * All three tensors are TRC_HIP_TYPE_F32 with 4-byte aligned data and strides.
- * The sum is reordered, so results match the CPU to rounding, not bit for bit. */
+ * The sum is reordered, so results match the CPU to rounding, not bit for bit;
+ * they are the same from run to run. dst must not overlap a or b: for some
+ * shapes it is cleared first and the halves of the sum over k are added into it. */
 int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b,
                         const trc_hip_tensor* dst, void* stream);
 
