@@ -213,3 +213,14 @@ def test_shape_errors_are_rejected(hip):
     with pytest.raises(H.HipError) as e:
         H.mul_mat_f32(a2.tensor(), b2.tensor(), d2.tensor())  # 3 % 2 != 0
     assert e.value.code == H.E_SHAPE
+    # dst sharing bytes with an operand
+    buf = empty((1, 1, 8, 8))  # a: K = 8, M = 8
+    b3 = empty((1, 1, 6, 8))   # b: K = 8, N = 6
+    with pytest.raises(H.HipError) as e:
+        H.mul_mat_f32(buf.tensor(), b3.tensor(), H.tensor(buf.ptr + 16, [8, 6, 1, 1], H.contiguous_nb([8, 6, 1, 1])))
+    assert e.value.code == H.E_SHAPE
+    with pytest.raises(H.HipError) as e:
+        H.mul_mat_f32(buf.tensor(), b3.tensor(), H.tensor(b3.ptr, [8, 6, 1, 1], H.contiguous_nb([8, 6, 1, 1])))
+    assert e.value.code == H.E_SHAPE
+    for t in (buf, b3):
+        t.free()

@@ -57,12 +57,15 @@ def test_config2_decode_shapes(hip, name, N):
 
 @pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("N", [1, 2])
-@pytest.mark.parametrize("K,M,w_off", [(32 * 130, 3001, 0), (32 * 264, 999, 4), (32 * 264, 999, 0), (512, 20000, 0)])
+@pytest.mark.parametrize("K,M,w_off", [(32 * 130, 3001, 0), (32 * 264, 999, 4), (32 * 264, 999, 0), (512, 20000, 0),
+                                       (32 * 200, 777, 0), (16384, 300, 0)])
 def test_dot_kernel_weight_paths(hip, name, N, K, M, w_off):
-    """The one- and two-column kernel's ways of reading W: into registers (130
+    """The one- and two-column kernels' ways of reading W: into registers (130
     blocks per row, not a multiple of 8; or W 4 bytes off a 16-byte boundary),
-    through LDS over two full chunks of 128 blocks and a short one (264 blocks),
-    and through LDS with more workgroups than CUs (20000 rows of 8 per wave)."""
+    through LDS over two full chunks of 128 blocks and a short one (264 blocks;
+    one column: one chunk per wave, a fourth slot idle), two chunks (200 blocks)
+    and four full ones (512 blocks), and through LDS with more workgroups than
+    CUs (20000 rows of 8 per wave)."""
     t = TYPES[name]
     announce(f"qmatvec dot paths {name} N={N} K={K} M={M} w_off={w_off}")
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 1000 + K + M))
@@ -175,16 +178,18 @@ def test_mfma_dynamic_range(hip, name):
 @pytest.mark.parametrize("name", ["q4_0", "q5_1", "q8_0"])
 @pytest.mark.parametrize("N", [1, 2, 4])
 @pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
-def test_nonfinite_x(hip, name, N, bad):
+@pytest.mark.parametrize("K", [256, 32 * 296])
+def test_nonfinite_x(hip, name, N, bad, K):
     """A non-finite x element makes its column non-finite, as in the reference
     (the fixed-point kernels return NaN there); the other columns are unaffected.
-    Covers the integer-dot (N = 1, 2) and fp16 MFMA (N = 4) kernels."""
+    Covers the integer-dot (N = 1, 2), one-chunk-per-wave (N = 1, 296 blocks:
+    the element sits in the third chunk) and fp16 MFMA (N = 4) kernels."""
     t = TYPES[name]
-    K, M = 256, 40
+    M = 40
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 8))
     X = synth.normal(9, K * N).reshape(1, 1, N, K)
     j = N - 1
-    X[0, 0, j, 37] = bad
+    X[0, 0, j, K - 219] = bad
     got = gpu_qmatvec(t, raw, K, M, X)
     want = oracle_qmatvec(t, raw, K, M, X)
     assert not np.isfinite(want[0, 0, j]).any()

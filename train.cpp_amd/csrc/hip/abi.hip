@@ -223,6 +223,18 @@ int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const 
                     (long long) b->ne[0], (long long) b->ne[1], (long long) b->ne[2], (long long) b->ne[3],
                     (long long) dst->ne[0], (long long) dst->ne[1], (long long) dst->ne[2], (long long) dst->ne[3]);
     }
+    // dst may be cleared before the sums are added into it, so it must not
+    // share bytes with an operand (compared by the byte spans the views cover)
+    auto span_end = [](const trc_hip_tensor* t) {
+        uintptr_t e = (uintptr_t) t->data + 4;
+        for (int i = 0; i < 4; ++i) e += (uintptr_t) (t->ne[i] - 1) * t->nb[i];
+        return e;
+    };
+    for (const trc_hip_tensor* t : {a, b}) {
+        if ((uintptr_t) dst->data < span_end(t) && (uintptr_t) t->data < span_end(dst)) {
+            return fail(TRC_HIP_E_SHAPE, "trc_hip_mul_mat_f32: dst overlaps an operand");
+        }
+    }
     return launch_mul_mat_f32(*a, *b, *dst, (hipStream_t) stream);
 }
 

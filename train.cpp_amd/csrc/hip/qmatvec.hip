@@ -1055,6 +1055,136 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         if (lane < RPW && row < M) y[n * ldy + row] = out[n];
 }
 
+// One column with K in 2..CS chunks of QD_CH blocks (the weights through LDS).
+// The 8 waves of a workgroup are QD_WAVES / CS groups of CS waves: wave (g, c)
+// takes chunk c of the rows of group g. All of x is converted once, each wave's
+// digit planes stay in registers, and no wave meets a chunk boundary, so its
+// copies stream without the drain k_qmatvec_dot has at every boundary. A row's
+// partial sums meet in LDS and are added in chunk order (deterministic).
+// Waves whose chunk is past the end copy nothing (an empty buffer range reads
+// zeros) and add zeros.
+template <int TYPE, int RPW, int CS, int PF_ROWS>
+__global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_kslots(const uint8_t* __restrict__ W, int64_t nblk,
+                                                                   int64_t M, int64_t nb1_w,
+                                                                   const float* __restrict__ x, float* __restrict__ y) {
+    constexpr int BYTES = block_bytes(TYPE);
+    constexpr int PW = QdFmt<TYPE>::PAIR_WORDS;
+    constexpr int PF = PF_ROWS < RPW ? PF_ROWS : RPW;
+    constexpr int SEG = QD_CH * BYTES;
+    constexpr int NI = (SEG + 1023) / 1024;
+    constexpr int SLOTS = PF + 1;
+    constexpr int G = QD_WAVES / CS;  // row groups per workgroup
+    static_assert(QD_WAVES % CS == 0 && RPW <= 64, "chunk slots divide the waves; one lane per row");
+    __shared__ __attribute__((aligned(16))) uint8_t wring[QD_WAVES][SLOTS][NI * 1024];
+    __shared__ __attribute__((aligned(16))) uint32_t planes[CS][(QD_CH / 2) * QD_PSTRIDE];
+    __shared__ float scale_l[CS][QD_CH];
+    __shared__ float xsum_l[CS][QD_CH];
+    __shared__ float part[QD_WAVES][RPW];
+
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = wv / CS, ch = wv % CS;
+    // rows strided over all groups, as the waves of k_qmatvec_dot
+    const int64_t group = (int64_t) blockIdx.x * G + g;
+    const int64_t n_groups = (int64_t) gridDim.x * G;
+    const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
+    auto chunk_blocks = [&](int64_t c) -> int64_t {
+        return c < nchunks ? (nblk - c * QD_CH < QD_CH ? nblk - c * QD_CH : QD_CH) : 0;
+    };
+    const int64_t cb = chunk_blocks(ch);
+    const bool mine = 2 * lane < cb;
+    const int pl = mine ? lane : (cb > 0 ? (int) (cb / 2) - 1 : 0);
+
+    int64_t roff[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int64_t row = group + r * n_groups;
+        roff[r] = (row < M ? row : M - 1) * nb1_w;
+    }
+    auto issue = [&](int r) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*) (W + roff[r] + ch * (int64_t) SEG), (short) 0, (int) cb * BYTES, QD_RSRC_WORD3);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) qd_dma16(rs, &wring[wv][r % SLOTS][i * 1024], (uint32_t) (i * 1024 + 16 * lane));
+    };
+
+    // x of every chunk (chunks past the end re-point at chunk 0 and convert as empty),
+    // then the first rows' copies, then the conversion
+    f4 xv[CS][4];
+    QdX4 xn[CS];
+#pragma unroll
+    for (int c = 0; c < CS; ++c) {
+        const float* xc = x + (c < nchunks ? c * QD_CH * QK : 0);
+        if constexpr (qd_nibble_path<TYPE>()) {
+            qd_load_x_n4<TYPE == TRC_HIP_TYPE_Q4_0>(xc, chunk_blocks(c), xn[c]);
+        } else {
+            qd_load_x(xc, chunk_blocks(c), xv[c]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < PF; ++r) issue(r);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < CS; ++c) {
+        if constexpr (qd_nibble_path<TYPE>()) {
+            qd_prologue_n4(xn[c], chunk_blocks(c), planes[c], scale_l[c], xsum_l[c]);
+        } else {
+            qd_prologue<TYPE == TRC_HIP_TYPE_Q8_0>(xv[c], chunk_blocks(c), planes[c], scale_l[c], xsum_l[c]);
+        }
+    }
+    qd_barrier();
+
+    // this wave's pair of its chunk (layout as in k_qmatvec_dot)
+    uint32_t PA[24], PB[24];
+    float sc[2], xs[2];
+    {
+        const uint32_t* src = planes[ch] + pl * QD_PSTRIDE;
+#pragma unroll
+        for (int k = 0; k < 12; ++k) {
+            const uint4 v = *(const uint4*) (src + 4 * k);
+            uint32_t* dst;
+            if constexpr (qd_nibble_path<TYPE>()) {
+                dst = k < 6 ? &PA[4 * k] : &PB[4 * (k - 6)];
+            } else {
+                const int p = k >> 2, gg = k & 3;
+                dst = gg < 2 ? &PA[8 * p + 4 * gg] : &PB[8 * p + 4 * (gg - 2)];
+            }
+            dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+        }
+        sc[0] = scale_l[ch][2 * pl];
+        sc[1] = scale_l[ch][2 * pl + 1];
+        xs[0] = xsum_l[ch][2 * pl];
+        xs[1] = xsum_l[ch][2 * pl + 1];
+    }
+
+    uint32_t w[PW];
+    float out = 0.f;  // lane r: this chunk's part of row r
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        if (r + PF < RPW) issue(r + PF);
+        __builtin_amdgcn_sched_barrier(0);  // row r + PF stays in flight during row r
+        qd_wait_rows<NI>(RPW - 1 - r < PF ? RPW - 1 - r : PF);
+        const uint32_t a = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t*) &wring[wv][r % SLOTS][0] +
+                           (uint32_t) pl * (PW * 4);
+        qd_lds_words<PW>(a, w);
+        const float v = qd_pair<TYPE>(w, PA, PB, sc, xs);
+        const float sum = wave_sum_lane63(mine ? v : 0.f);
+        const float s63 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 63));
+        out = lane == r ? s63 : out;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (lane < RPW) part[wv][lane] = out;
+    qd_barrier();
+    if (ch == 0) {
+        const int r = lane < RPW ? lane : 0;
+        float s = part[g * CS][r];
+#pragma unroll
+        for (int c = 1; c < CS; ++c) s += part[g * CS + c][r];
+        const int64_t row = group + (int64_t) lane * n_groups;
+        if (lane < RPW && row < M) y[row] = s;
+    }
+}
+
 template <int TYPE, int RPW, int NC>
 int launch_dot_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, float* y,
                    size_t nb1_y, hipStream_t s) {
@@ -1106,6 +1236,38 @@ int launch_qmatvec_dot(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, co
     }
 }
 
+template <int TYPE, int RPW, int CS>
+int launch_kslots_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y,
+                      hipStream_t s) {
+    constexpr int G = QD_WAVES / CS;
+    // two rows in flight (one for Q8_0, whose 5 KiB ring slots would not fit
+    // beside all four chunks' planes)
+    constexpr int PF = TYPE == TRC_HIP_TYPE_Q8_0 ? 1 : 2;
+    const int64_t grid = (M + (int64_t) G * RPW - 1) / ((int64_t) G * RPW);
+    hipLaunchKernelGGL((k_qmatvec_kslots<TYPE, RPW, CS, PF>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s,
+                       (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, y);
+    return check_launch("qmatvec_kslots");
+}
+
+template <int TYPE, int CS>
+int launch_kslots(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y, hipStream_t s) {
+    // spread the rows evenly over the row groups of one workgroup per CU, at most QD_RMAX each
+    const int64_t groups = (int64_t) device_cus() * (QD_WAVES / CS);
+    int64_t rpw = (M + groups - 1) / groups;
+    if (rpw > QD_RMAX) rpw = QD_RMAX;
+    if (rpw < 1) rpw = 1;
+    switch (rpw) {
+        case 1: return launch_kslots_rpw<TYPE, 1, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 2: return launch_kslots_rpw<TYPE, 2, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 3: return launch_kslots_rpw<TYPE, 3, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 4: return launch_kslots_rpw<TYPE, 4, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 5: return launch_kslots_rpw<TYPE, 5, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 6: return launch_kslots_rpw<TYPE, 6, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 7: return launch_kslots_rpw<TYPE, 7, CS>(wq, nblk, M, nb1_w, x, y, s);
+        default: return launch_kslots_rpw<TYPE, 8, CS>(wq, nblk, M, nb1_w, x, y, s);
+    }
+}
+
 int qv1_grid(int64_t M, int rows) {
     const int cus = device_cus();
     const int64_t tiles = (M + rows - 1) / rows;
@@ -1134,6 +1296,20 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
     // 4-byte boundaries and x columns on 16-byte ones
     const bool dot_ok = nblk % 2 == 0 && (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0 &&
                         (((uintptr_t) x) & 15u) == 0 && (nb1_x & 15u) == 0;
+    // N = 1 with K in 2..4 chunks of 128 blocks, weights through LDS: one chunk
+    // per wave, when one workgroup per CU covers M (measured at M = 4096: K =
+    // 8192..16384 8-19 % faster for the 4- and 5-bit formats; with more
+    // workgroups than CUs 27-39 % slower, as each holds ~130 KB of LDS; Q8_0,
+    // with one row in flight, no faster)
+    const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
+    const bool lds_ok = nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0;
+    if (dot_ok && lds_ok && N == 1 && TYPE != TRC_HIP_TYPE_Q8_0 && nchunks >= 2 && nchunks <= 4) {
+        const int cs = nchunks == 2 ? 2 : 4;
+        if (M <= (int64_t) device_cus() * (QD_WAVES / cs) * QD_RMAX) {
+            return cs == 2 ? launch_kslots<TYPE, 2>(wq, nblk, M, nb1_w, x, y, s)
+                           : launch_kslots<TYPE, 4>(wq, nblk, M, nb1_w, x, y, s);
+        }
+    }
     if (dot_ok && N == 1) return launch_qmatvec_dot<TYPE, 1>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
     if (dot_ok && N == 2) return launch_qmatvec_dot<TYPE, 2>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
     // 3 <= N <= 32 (and N = 2 off the dot kernel's alignment): fp16 matrix-core kernel (qmm.hip)
