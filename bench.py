@@ -8,7 +8,8 @@ batch. Algorithmic bytes per step = W blocks + x + y = 33,103,872 B.
 
 The same run also measures, each against its roofline (`extra`):
   - bulk dequant of all five formats on 4096 x 11008 (configuration 1), GB/s;
-  - the fused kernel for Q4_0/Q5_0 at N = 1 and 16 (configuration 2);
+  - the fused kernel for Q4_0/Q5_0 at N = 1 and 16 (configuration 2), Q4_0 at
+    N = 64, and configuration 0's product (Q8_0 [4096, 4096] times 8 columns);
   - the F32 mul_mat forward + both backward products of a 4096x4096 linear
     layer over 512 tokens (configuration 3) and the batched broadcast product
     with a permuted src1 (configuration 4), TFLOP/s on the FP32 MFMA roofline.
@@ -150,9 +151,9 @@ def rotation_count(bytes_per_set: int, floor: int = 3, target: int = 512 << 20) 
     return max(floor, -(-target // max(bytes_per_set, 1)) + 1)
 
 
-def qmatvec_case(H, synth, timer, t, K, M, N, steps, warmup):
-    blk = synth.block_bytes(synth.quant_blocks(t, K * M // 32, synth.config_seed(2, t)))
-    x = synth.normal(synth.config_seed(2, 100 + N), K * N)
+def qmatvec_case(H, synth, timer, t, K, M, N, steps, warmup, cfg=2):
+    blk = synth.block_bytes(synth.quant_blocks(t, K * M // 32, synth.config_seed(cfg, t)))
+    x = synth.normal(synth.config_seed(cfg, 100 + N), K * N)
     alg_bytes = blk.nbytes + x.nbytes + M * N * 4
     sets = rotation_count(alg_bytes)
     ws = [H.DeviceBuffer(blk.nbytes).upload(blk) for _ in range(sets)]
@@ -431,6 +432,9 @@ def main():
         # skinny GEMM at the top of the fused range (one pass over W per 32 columns)
         r, _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 64, s, w)
         extra["qmatvec"]["q4_0 N=64"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+        # configuration 0's product: Q8_0 W[4096,4096] times x with 8 columns, fused
+        r, _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q8_0, 4096, 4096, 8, s, w, cfg=0)
+        extra["qmatvec_cfg0_q8_0_4096x4096_n8"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
         extra["dequant_4096x11008"] = {}
         for name, t in H.QUANT_TYPES.items():
             r = dequant_case(H, synth, timer, t, 4096 * 11008 // 32, s, w)
