@@ -46,7 +46,8 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
                        hipStream_t stream);
 int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x,
                    int64_t N, size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream);
-// Fused quant x skinny GEMM on the fp16 matrix cores for 2 <= N <= 32
+// Fused quant x skinny GEMM on the fp16 matrix cores for 2 <= N <= 32 (N = 2, 3
+// only off the integer-dot kernel's alignment)
 // (qmm.hip); qmm_supported says whether the shape and alignment fit it.
 bool qmm_supported(int64_t K, int64_t N, const void* wq, size_t nb1_w);
 int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
