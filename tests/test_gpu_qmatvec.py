@@ -56,12 +56,13 @@ def test_config2_decode_shapes(hip, name, N):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
-@pytest.mark.parametrize("N", [1, 2, 3])
+@pytest.mark.parametrize("N", [1, 2, 3, 4])
 @pytest.mark.parametrize("K,M,w_off", [(32 * 130, 3001, 0), (32 * 264, 999, 4), (32 * 264, 999, 0), (512, 20000, 0),
                                        (32 * 200, 777, 0), (16384, 300, 0)])
 def test_dot_kernel_weight_paths(hip, name, N, K, M, w_off):
-    """The one- to three-column kernels' ways of reading W (three columns only
-    through LDS; the other cases take the matrix-core kernel): into registers (130
+    """The one- to four-column kernels' ways of reading W (three and four
+    columns only through LDS, four only within one chunk and not for Q4_0; the
+    other cases take the matrix-core kernel): into registers (130
     blocks per row, not a multiple of 8; or W 4 bytes off a 16-byte boundary),
     through LDS over two full chunks of 128 blocks and a short one (264 blocks;
     one column: one chunk per wave, a fourth slot idle), two chunks (200 blocks)

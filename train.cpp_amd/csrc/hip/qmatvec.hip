@@ -928,14 +928,12 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         roff[r] = (row < M ? row : M - 1) * nb1_w;
     }
 
-    float acc[NC][RPW];
-    float out[NC];  // lane r: row r's result
+    // lane r: row r's result, the chunks' wave sums added in chunk order (no
+    // per-lane accumulators across chunks, which leaves registers for the
+    // columns' digit planes)
+    float out[NC];
 #pragma unroll
-    for (int n = 0; n < NC; ++n) {
-        out[n] = 0.f;
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[n][r] = 0.f;
-    }
+    for (int n = 0; n < NC; ++n) out[n] = 0.f;
 
     const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
     uint32_t w[DMA ? 1 : RPW][PW];
@@ -1028,20 +1026,14 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
             if (r + PF < RPW) issue(r + PF);
             __builtin_amdgcn_sched_barrier(0);  // row r + PF stays in flight during row r
             const uint32_t* wr = pair_words(r);
+            // reduce this chunk's part of row r while the next rows' loads are
+            // in flight and add it into lane r
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
                 const float v = qd_pair<TYPE>(wr, PA[n], PB[n], sc[n], xs[n]);
-                acc[n][r] += mine ? v : 0.f;
-            }
-            // after the last chunk a row is final: reduce it while the next
-            // rows' loads are in flight and keep the sum in lane r
-            if (c == nchunks - 1) {
-#pragma unroll
-                for (int n = 0; n < NC; ++n) {
-                    const float sum = wave_sum_lane63(acc[n][r]);
-                    const float s63 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 63));
-                    out[n] = lane == r ? s63 : out[n];
-                }
+                const float sum = wave_sum_lane63(mine ? v : 0.f);
+                const float s63 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 63));
+                out[n] = lane == r ? (c == 0 ? s63 : out[n] + s63) : out[n];
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -1293,10 +1285,10 @@ template <int TYPE>
 int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N, size_t nb1_x,
                 float* y, size_t nb1_y, hipStream_t s) {
     const int64_t nblk = K / QK;
-    // N = 1..3: integer-dot kernel (one pass over W for all columns; each
-    // column's digit planes take 48 registers, so a third column fits only when
-    // the weights come through LDS, and a fourth spills); pairs of blocks start
-    // on 4-byte boundaries and x columns on 16-byte ones
+    // N = 1..4: integer-dot kernel (one pass over W for all columns; each
+    // column's digit planes take 48 registers, so a third and fourth column fit
+    // only when the weights come through LDS); pairs of blocks start on 4-byte
+    // boundaries and x columns on 16-byte ones
     const bool dot_ok = nblk % 2 == 0 && (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0 &&
                         (((uintptr_t) x) & 15u) == 0 && (nb1_x & 15u) == 0;
     // N = 1 with K in 2..4 chunks of 128 blocks, weights through LDS: one chunk
@@ -1318,6 +1310,12 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
     // three columns: 21-33 % faster than the fp16 matrix-core kernel (measured,
     // all formats at K = 4096, M = 14336)
     if (dot_ok && lds_ok && N == 3) return launch_qmatvec_dot<TYPE, 3>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+    // four columns fill the registers (Q5_1 spills 8 bytes per lane, Q4_0 44):
+    // 9-24 % faster than the matrix-core kernel for Q4_1, Q5_0, Q5_1 and Q8_0
+    // with K in one chunk; Q4_0 10 % slower, and 45 % slower over three chunks
+    if (dot_ok && lds_ok && N == 4 && TYPE != TRC_HIP_TYPE_Q4_0 && nchunks == 1) {
+        return launch_qmatvec_dot<TYPE, 4>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+    }
     // 3 <= N <= 32 (and N = 2 off the dot kernel's alignment): fp16 matrix-core kernel (qmm.hip)
     if (qmm_supported(K, N, wq, nb1_w)) return launch_qmm(TYPE, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s);
     // N = 1 streaming kernel: needs 16-byte aligned rows and row chunks
