@@ -1243,12 +1243,16 @@ int launch_kslots_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, con
     return check_launch("qmatvec_kslots");
 }
 
+// Rows per wave of k_qmatvec_kslots at most (its waves hold one chunk's planes
+// and one row's words, so more rows cost only their row offsets).
+constexpr int QK_RMAX = 16;
+
 template <int TYPE, int CS>
 int launch_kslots(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y, hipStream_t s) {
-    // spread the rows evenly over the row groups of one workgroup per CU, at most QD_RMAX each
+    // spread the rows evenly over the row groups of one workgroup per CU, at most QK_RMAX each
     const int64_t groups = (int64_t) device_cus() * (QD_WAVES / CS);
     int64_t rpw = (M + groups - 1) / groups;
-    if (rpw > QD_RMAX) rpw = QD_RMAX;
+    if (rpw > QK_RMAX) rpw = QK_RMAX;
     if (rpw < 1) rpw = 1;
     switch (rpw) {
         case 1: return launch_kslots_rpw<TYPE, 1, CS>(wq, nblk, M, nb1_w, x, y, s);
@@ -1258,7 +1262,11 @@ int launch_kslots(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const f
         case 5: return launch_kslots_rpw<TYPE, 5, CS>(wq, nblk, M, nb1_w, x, y, s);
         case 6: return launch_kslots_rpw<TYPE, 6, CS>(wq, nblk, M, nb1_w, x, y, s);
         case 7: return launch_kslots_rpw<TYPE, 7, CS>(wq, nblk, M, nb1_w, x, y, s);
-        default: return launch_kslots_rpw<TYPE, 8, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 8: return launch_kslots_rpw<TYPE, 8, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 9: case 10: return launch_kslots_rpw<TYPE, 10, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 11: case 12: return launch_kslots_rpw<TYPE, 12, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 13: case 14: return launch_kslots_rpw<TYPE, 14, CS>(wq, nblk, M, nb1_w, x, y, s);
+        default: return launch_kslots_rpw<TYPE, 16, CS>(wq, nblk, M, nb1_w, x, y, s);
     }
 }
 
@@ -1292,15 +1300,16 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
     const bool dot_ok = nblk % 2 == 0 && (((uintptr_t) wq) & 3u) == 0 && (nb1_w & 3u) == 0 &&
                         (((uintptr_t) x) & 15u) == 0 && (nb1_x & 15u) == 0;
     // N = 1 with K in 2..4 chunks of 128 blocks, weights through LDS: one chunk
-    // per wave, when one workgroup per CU covers M (measured at M = 4096: K =
-    // 8192..16384 8-19 % faster for the 4- and 5-bit formats; with more
+    // per wave, when one workgroup per CU covers M with up to 16 rows per wave
+    // (measured: K = 8192..16384 at M = 4096 8-19 % faster for the 4- and 5-bit
+    // formats, K = 13824 at M = 5120 22 %, K = 14336 at M = 8192 6 %; with more
     // workgroups than CUs 27-39 % slower, as each holds ~130 KB of LDS; Q8_0,
     // with one row in flight, no faster)
     const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
     const bool lds_ok = nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0;
     if (dot_ok && lds_ok && N == 1 && TYPE != TRC_HIP_TYPE_Q8_0 && nchunks >= 2 && nchunks <= 4) {
         const int cs = nchunks == 2 ? 2 : 4;
-        if (M <= (int64_t) device_cus() * (QD_WAVES / cs) * QD_RMAX) {
+        if (M <= (int64_t) device_cus() * (QD_WAVES / cs) * QK_RMAX) {
             return cs == 2 ? launch_kslots<TYPE, 2>(wq, nblk, M, nb1_w, x, y, s)
                            : launch_kslots<TYPE, 4>(wq, nblk, M, nb1_w, x, y, s);
         }
