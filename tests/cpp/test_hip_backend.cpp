@@ -486,14 +486,15 @@ void test_gguf_config0(Device* dev, const std::string& dir) {
 }
 
 // Quantized tensors inside graphs: raw blocks loaded as Q4_0/Q5_0/..., then
-// cast to F32 (dequant node) and mul_mat with F32 activations (fused kernel
-// for N <= 16, dequantize + MFMA otherwise).
+// cast to F32 (dequant node) and mul_mat with F32 activations (the fused
+// kernels up to 64 columns: integer dots for 1-4, fp16 MFMA above; dequantize
+// + F32 MFMA beyond).
 void test_quantized_graph(Device* dev, const std::string& dir) {
     std::printf("quantized tensors in graphs\n");
     const Type types[] = {TYPE_Q4_0, TYPE_Q4_1, TYPE_Q5_0, TYPE_Q5_1, TYPE_Q8_0};
     const int64_t K = 512, M = 96;
     for (Type qt : types) {
-        for (int64_t N : {1, 5, 16, 40}) {
+        for (int64_t N : {1, 3, 4, 5, 16, 40, 80}) {
             const std::vector<uint8_t> blocks = quant_blocks(qt, K * M / 32, 77 + (uint64_t) qt);
             const std::string path = dir + "/q_" + type_name(qt) + ".gguf";
             EXPECT(write_gguf(path, "w", qt, {K, M}, blocks, false));
