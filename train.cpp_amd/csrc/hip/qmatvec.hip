@@ -485,11 +485,22 @@ struct QdFmt {
 
 // x chunk -> byte planes in LDS. Thread t converts elements [16t, 16t+16) of
 // the chunk: half h = t&1 of block b = t>>1 (partner lane t^1 holds the other half).
+// x of a chunk through a buffer range of its cb blocks: threads past a short
+// (or empty) chunk read zeros from the range check, with no memory access and
+// no branch (loads under a branch make the compiler's wait counts fall back to
+// full waits, which serialised the x loads of several chunks).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t qd_x_range(const float* xc, int64_t cb) {
+    // raw 32-bit dwords (gfx9 buffer resource word 3), cb blocks of 32 floats
+    return __builtin_amdgcn_make_buffer_rsrc((void*) xc, (short) 0, (int) cb * QK * 4, 0x00020000u);
+}
+
 __device__ __forceinline__ void qd_load_x(const float* __restrict__ xc, int64_t cb, f4* v) {
     const int t = threadIdx.x;
-    const bool active = (t >> 1) < cb;
+    const __amdgpu_buffer_rsrc_t rs = qd_x_range(xc, cb);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = active ? ((const f4*) xc)[4 * t + i] : f4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 4; ++i) {
+        v[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t) (4 * t + i) * 16, 0, 0));
+    }
 }
 
 // SIGNED: balanced digits X = D0 + 256 D1 + 65536 D2 with every D in [-128, 127]
@@ -497,7 +508,9 @@ __device__ __forceinline__ void qd_load_x(const float* __restrict__ xc, int64_t 
 // (0 < U < 2^24) are D + 128, so the planes of U with each byte's top bit
 // flipped are the digits. Otherwise P0, P1 are the unsigned low bytes of X and
 // P2 its signed top byte (for the unsigned nibble quants and v_dot4_u32_u8).
-template <bool SIGNED>
+// PS: LDS dwords per pair of planes (48, or QD_PSTRIDE with the padding that
+// makes the once-per-chunk 16-byte reads conflict-free).
+template <bool SIGNED, int PS = QD_PSTRIDE>
 __device__ __forceinline__ void qd_prologue(const f4* v, int64_t cb, uint32_t* planes, float* scale, float* xsum) {
     const int t = threadIdx.x;
     const int b = t >> 1, h = t & 1;
@@ -538,7 +551,7 @@ __device__ __forceinline__ void qd_prologue(const f4* v, int64_t cb, uint32_t* p
     if (active) {
         // pair l = b>>1; within the pair, block (b&1) owns groups 8*(b&1) .. +7:
         // groups 0-3 are elements 0-15 (half 0), groups 4-7 elements 16-31 (half 1)
-        uint32_t* dst = planes + (b >> 1) * QD_PSTRIDE + 8 * (b & 1) + 4 * h;
+        uint32_t* dst = planes + (b >> 1) * PS + 8 * (b & 1) + 4 * h;
 #pragma unroll
         for (int p = 0; p < 3; ++p) {
             *(uint4*) (dst + 16 * p) = uint4{P[p][0], P[p][1], P[p][2], P[p][3]};
@@ -586,15 +599,17 @@ __device__ __forceinline__ void qd_load_x_n4(const float* __restrict__ xc, int64
     const bool order_a = ORDER_A_EVEN && (b & 1) == 0;
     const int j0 = order_a ? (g == 0 ? 0 : 4 * g - 2) : 4 * g;
     const int j1 = order_a ? (g == 0 ? 14 : 4 * g) : 4 * g + 2;
-    const bool active = b < cb;
-    const float2* xb = (const float2*) (xc + 32 * (active ? b : 0));
-    const float2 z = {0.f, 0.f};
-    x.v[0] = active ? xb[j0 >> 1] : z;
-    x.v[1] = active ? xb[j1 >> 1] : z;
-    x.v[2] = active ? xb[(j0 + 16) >> 1] : z;
-    x.v[3] = active ? xb[(j1 + 16) >> 1] : z;
+    // zeros past a short chunk from the range check (see qd_load_x)
+    const __amdgpu_buffer_rsrc_t rs = qd_x_range(xc, cb);
+    const uint32_t base = (uint32_t) (32 * b) * 4;
+    const int js[4] = {j0, j1, j0 + 16, j1 + 16};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        x.v[k] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rs, base + (uint32_t) (js[k] >> 1) * 8, 0, 0));
+    }
 }
 
+template <int PS = QD_PSTRIDE>
 __device__ __forceinline__ void qd_prologue_n4(const QdX4& x, int64_t cb, uint32_t* planes, float* scale, float* xsum) {
     const int t = threadIdx.x;
     const int b = t >> 2, g = t & 3;
@@ -628,7 +643,7 @@ __device__ __forceinline__ void qd_prologue_n4(const QdX4& x, int64_t cb, uint32
         uint32_t BL[3], BH[3];
         bytes3_of4(U[0], U[1], U[2], U[3], BL);
         bytes3_of4(U[4], U[5], U[6], U[7], BH);
-        uint32_t* dst = planes + (b >> 1) * QD_PSTRIDE + 24 * (b & 1) + g;
+        uint32_t* dst = planes + (b >> 1) * PS + 24 * (b & 1) + g;
 #pragma unroll
         for (int y = 0; y < 3; ++y) {
             dst[8 * y] = (BL[y] & 0x0F0F0F0Fu) | ((BH[y] & 0x0F0F0F0Fu) << 4);
@@ -1047,18 +1062,20 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
         if (lane < RPW && row < M) y[n * ldy + row] = out[n];
 }
 
-// One column with K in 2..CS chunks of QD_CH blocks (the weights through LDS).
-// The 8 waves of a workgroup are QD_WAVES / CS groups of CS waves: wave (g, c)
-// takes chunk c of the rows of group g. All of x is converted once, each wave's
-// digit planes stay in registers, and no wave meets a chunk boundary, so its
-// copies stream without the drain k_qmatvec_dot has at every boundary. A row's
-// partial sums meet in LDS and are added in chunk order (deterministic).
-// Waves whose chunk is past the end copy nothing (an empty buffer range reads
-// zeros) and add zeros.
-template <int TYPE, int RPW, int CS, int PF_ROWS>
+// One or two columns with K in 2..CS chunks of QD_CH blocks (the weights
+// through LDS). The 8 waves of a workgroup are QD_WAVES / CS groups of CS
+// waves: wave (g, c) takes chunk c of the rows of group g. All of x is
+// converted once, each wave's digit planes stay in registers, and no wave meets
+// a chunk boundary, so its copies stream without the drain k_qmatvec_dot has at
+// every boundary. A row's partial sums meet in LDS and are added in chunk
+// order (deterministic). Waves whose chunk is past the end copy nothing (an
+// empty buffer range reads zeros) and add zeros. Two columns' planes of four
+// chunks fit only without the plane rows' padding (48 dwords per pair).
+template <int TYPE, int RPW, int CS, int PF_ROWS, int NC>
 __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_kslots(const uint8_t* __restrict__ W, int64_t nblk,
                                                                    int64_t M, int64_t nb1_w,
-                                                                   const float* __restrict__ x, float* __restrict__ y) {
+                                                                   const float* __restrict__ x, int64_t ldx,
+                                                                   float* __restrict__ y, int64_t ldy) {
     constexpr int BYTES = block_bytes(TYPE);
     constexpr int PW = QdFmt<TYPE>::PAIR_WORDS;
     constexpr int PF = PF_ROWS < RPW ? PF_ROWS : RPW;
@@ -1066,12 +1083,13 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_kslots(const uint8_t*
     constexpr int NI = (SEG + 1023) / 1024;
     constexpr int SLOTS = PF + 1;
     constexpr int G = QD_WAVES / CS;  // row groups per workgroup
+    constexpr int PS = NC > 1 ? 48 : QD_PSTRIDE;
     static_assert(QD_WAVES % CS == 0 && RPW <= 64, "chunk slots divide the waves; one lane per row");
     __shared__ __attribute__((aligned(16))) uint8_t wring[QD_WAVES][SLOTS][NI * 1024];
-    __shared__ __attribute__((aligned(16))) uint32_t planes[CS][(QD_CH / 2) * QD_PSTRIDE];
-    __shared__ float scale_l[CS][QD_CH];
-    __shared__ float xsum_l[CS][QD_CH];
-    __shared__ float part[QD_WAVES][RPW];
+    __shared__ __attribute__((aligned(16))) uint32_t planes[CS][NC][(QD_CH / 2) * PS];
+    __shared__ float scale_l[CS][NC][QD_CH];
+    __shared__ float xsum_l[CS][NC][QD_CH];
+    __shared__ float part[QD_WAVES][NC][RPW];
 
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1100,17 +1118,20 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_kslots(const uint8_t*
         for (int i = 0; i < NI; ++i) qd_dma16(rs, &wring[wv][r % SLOTS][i * 1024], (uint32_t) (i * 1024 + 16 * lane));
     };
 
-    // x of every chunk (chunks past the end re-point at chunk 0 and convert as empty),
-    // then the first rows' copies, then the conversion
-    f4 xv[CS][4];
-    QdX4 xn[CS];
+    // x of every chunk and column (chunks past the end re-point at chunk 0 and
+    // convert as empty), then the first rows' copies, then the conversion
+    f4 xv[CS][NC][4];
+    QdX4 xn[CS][NC];
 #pragma unroll
     for (int c = 0; c < CS; ++c) {
-        const float* xc = x + (c < nchunks ? c * QD_CH * QK : 0);
-        if constexpr (qd_nibble_path<TYPE>()) {
-            qd_load_x_n4<TYPE == TRC_HIP_TYPE_Q4_0>(xc, chunk_blocks(c), xn[c]);
-        } else {
-            qd_load_x(xc, chunk_blocks(c), xv[c]);
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            const float* xc = x + n * ldx + (c < nchunks ? c * QD_CH * QK : 0);
+            if constexpr (qd_nibble_path<TYPE>()) {
+                qd_load_x_n4<TYPE == TRC_HIP_TYPE_Q4_0>(xc, chunk_blocks(c), xn[c][n]);
+            } else {
+                qd_load_x(xc, chunk_blocks(c), xv[c][n]);
+            }
         }
     }
 #pragma unroll
@@ -1118,39 +1139,46 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_kslots(const uint8_t*
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int c = 0; c < CS; ++c) {
-        if constexpr (qd_nibble_path<TYPE>()) {
-            qd_prologue_n4(xn[c], chunk_blocks(c), planes[c], scale_l[c], xsum_l[c]);
-        } else {
-            qd_prologue<TYPE == TRC_HIP_TYPE_Q8_0>(xv[c], chunk_blocks(c), planes[c], scale_l[c], xsum_l[c]);
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            if constexpr (qd_nibble_path<TYPE>()) {
+                qd_prologue_n4<PS>(xn[c][n], chunk_blocks(c), planes[c][n], scale_l[c][n], xsum_l[c][n]);
+            } else {
+                qd_prologue<TYPE == TRC_HIP_TYPE_Q8_0, PS>(xv[c][n], chunk_blocks(c), planes[c][n], scale_l[c][n],
+                                                          xsum_l[c][n]);
+            }
         }
     }
     qd_barrier();
 
-    // this wave's pair of its chunk (layout as in k_qmatvec_dot)
-    uint32_t PA[24], PB[24];
-    float sc[2], xs[2];
-    {
-        const uint32_t* src = planes[ch] + pl * QD_PSTRIDE;
+    // this wave's pair of its chunk, per column (layout as in k_qmatvec_dot)
+    uint32_t PA[NC][24], PB[NC][24];
+    float sc[NC][2], xs[NC][2];
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+        const uint32_t* src = planes[ch][n] + pl * PS;
 #pragma unroll
         for (int k = 0; k < 12; ++k) {
             const uint4 v = *(const uint4*) (src + 4 * k);
             uint32_t* dst;
             if constexpr (qd_nibble_path<TYPE>()) {
-                dst = k < 6 ? &PA[4 * k] : &PB[4 * (k - 6)];
+                dst = k < 6 ? &PA[n][4 * k] : &PB[n][4 * (k - 6)];
             } else {
                 const int p = k >> 2, gg = k & 3;
-                dst = gg < 2 ? &PA[8 * p + 4 * gg] : &PB[8 * p + 4 * (gg - 2)];
+                dst = gg < 2 ? &PA[n][8 * p + 4 * gg] : &PB[n][8 * p + 4 * (gg - 2)];
             }
             dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
         }
-        sc[0] = scale_l[ch][2 * pl];
-        sc[1] = scale_l[ch][2 * pl + 1];
-        xs[0] = xsum_l[ch][2 * pl];
-        xs[1] = xsum_l[ch][2 * pl + 1];
+        sc[n][0] = scale_l[ch][n][2 * pl];
+        sc[n][1] = scale_l[ch][n][2 * pl + 1];
+        xs[n][0] = xsum_l[ch][n][2 * pl];
+        xs[n][1] = xsum_l[ch][n][2 * pl + 1];
     }
 
     uint32_t w[PW];
-    float out = 0.f;  // lane r: this chunk's part of row r
+    float out[NC];  // lane r: this chunk's part of row r
+#pragma unroll
+    for (int n = 0; n < NC; ++n) out[n] = 0.f;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         if (r + PF < RPW) issue(r + PF);
@@ -1159,21 +1187,29 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_kslots(const uint8_t*
         const uint32_t a = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t*) &wring[wv][r % SLOTS][0] +
                            (uint32_t) pl * (PW * 4);
         qd_lds_words<PW>(a, w);
-        const float v = qd_pair<TYPE>(w, PA, PB, sc, xs);
-        const float sum = wave_sum_lane63(mine ? v : 0.f);
-        const float s63 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 63));
-        out = lane == r ? s63 : out;
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            const float v = qd_pair<TYPE>(w, PA[n], PB[n], sc[n], xs[n]);
+            const float sum = wave_sum_lane63(mine ? v : 0.f);
+            const float s63 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 63));
+            out[n] = lane == r ? s63 : out[n];
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (lane < RPW) part[wv][lane] = out;
+#pragma unroll
+    for (int n = 0; n < NC; ++n)
+        if (lane < RPW) part[wv][n][lane] = out[n];
     qd_barrier();
     if (ch == 0) {
         const int r = lane < RPW ? lane : 0;
-        float s = part[g * CS][r];
-#pragma unroll
-        for (int c = 1; c < CS; ++c) s += part[g * CS + c][r];
         const int64_t row = group + (int64_t) lane * n_groups;
-        if (lane < RPW && row < M) y[row] = s;
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            float s = part[g * CS][n][r];
+#pragma unroll
+            for (int c = 1; c < CS; ++c) s += part[g * CS + c][n][r];
+            if (lane < RPW && row < M) y[n * ldy + row] = s;
+        }
     }
 }
 
@@ -1230,16 +1266,17 @@ int launch_qmatvec_dot(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, co
     }
 }
 
-template <int TYPE, int RPW, int CS>
-int launch_kslots_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y,
-                      hipStream_t s) {
+template <int TYPE, int RPW, int CS, int NC>
+int launch_kslots_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, float* y,
+                      size_t nb1_y, hipStream_t s) {
     constexpr int G = QD_WAVES / CS;
-    // two rows in flight (one for Q8_0, whose 5 KiB ring slots would not fit
-    // beside all four chunks' planes)
-    constexpr int PF = TYPE == TRC_HIP_TYPE_Q8_0 ? 1 : 2;
+    // two rows in flight for one column; one for two columns, as in
+    // k_qmatvec_dot (and their planes leave room for no more)
+    constexpr int PF = NC > 1 ? 1 : 2;
     const int64_t grid = (M + (int64_t) G * RPW - 1) / ((int64_t) G * RPW);
-    hipLaunchKernelGGL((k_qmatvec_kslots<TYPE, RPW, CS, PF>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s,
-                       (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, y);
+    hipLaunchKernelGGL((k_qmatvec_kslots<TYPE, RPW, CS, PF, NC>), dim3((unsigned) grid), dim3(QD_WAVES * 64), 0, s,
+                       (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, x, (int64_t) (nb1_x / sizeof(float)), y,
+                       (int64_t) (nb1_y / sizeof(float)));
     return check_launch("qmatvec_kslots");
 }
 
@@ -1247,26 +1284,27 @@ int launch_kslots_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, con
 // and one row's words, so more rows cost only their row offsets).
 constexpr int QK_RMAX = 16;
 
-template <int TYPE, int CS>
-int launch_kslots(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, float* y, hipStream_t s) {
+template <int TYPE, int CS, int NC>
+int launch_kslots(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, float* y,
+                  size_t nb1_y, hipStream_t s) {
     // spread the rows evenly over the row groups of one workgroup per CU, at most QK_RMAX each
     const int64_t groups = (int64_t) device_cus() * (QD_WAVES / CS);
     int64_t rpw = (M + groups - 1) / groups;
     if (rpw > QK_RMAX) rpw = QK_RMAX;
     if (rpw < 1) rpw = 1;
     switch (rpw) {
-        case 1: return launch_kslots_rpw<TYPE, 1, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 2: return launch_kslots_rpw<TYPE, 2, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 3: return launch_kslots_rpw<TYPE, 3, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 4: return launch_kslots_rpw<TYPE, 4, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 5: return launch_kslots_rpw<TYPE, 5, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 6: return launch_kslots_rpw<TYPE, 6, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 7: return launch_kslots_rpw<TYPE, 7, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 8: return launch_kslots_rpw<TYPE, 8, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 9: case 10: return launch_kslots_rpw<TYPE, 10, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 11: case 12: return launch_kslots_rpw<TYPE, 12, CS>(wq, nblk, M, nb1_w, x, y, s);
-        case 13: case 14: return launch_kslots_rpw<TYPE, 14, CS>(wq, nblk, M, nb1_w, x, y, s);
-        default: return launch_kslots_rpw<TYPE, 16, CS>(wq, nblk, M, nb1_w, x, y, s);
+        case 1: return launch_kslots_rpw<TYPE, 1, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 2: return launch_kslots_rpw<TYPE, 2, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 3: return launch_kslots_rpw<TYPE, 3, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 4: return launch_kslots_rpw<TYPE, 4, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 5: return launch_kslots_rpw<TYPE, 5, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 6: return launch_kslots_rpw<TYPE, 6, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 7: return launch_kslots_rpw<TYPE, 7, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 8: return launch_kslots_rpw<TYPE, 8, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 9: case 10: return launch_kslots_rpw<TYPE, 10, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 11: case 12: return launch_kslots_rpw<TYPE, 12, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        case 13: case 14: return launch_kslots_rpw<TYPE, 14, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+        default: return launch_kslots_rpw<TYPE, 16, CS, NC>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
     }
 }
 
@@ -1307,11 +1345,19 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
     // with one row in flight, no faster)
     const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
     const bool lds_ok = nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0;
-    if (dot_ok && lds_ok && N == 1 && TYPE != TRC_HIP_TYPE_Q8_0 && nchunks >= 2 && nchunks <= 4) {
-        const int cs = nchunks == 2 ? 2 : 4;
-        if (M <= (int64_t) device_cus() * (QD_WAVES / cs) * QK_RMAX) {
-            return cs == 2 ? launch_kslots<TYPE, 2>(wq, nblk, M, nb1_w, x, y, s)
-                           : launch_kslots<TYPE, 4>(wq, nblk, M, nb1_w, x, y, s);
+    // two columns only over four chunks (K = 13824 at M = 5120: 17 % faster,
+    // K = 14336 at M = 4096: 7 %; over two or three chunks 2-20 % slower)
+    if constexpr (TYPE != TRC_HIP_TYPE_Q8_0) {
+        if (dot_ok && lds_ok && (N == 1 || (N == 2 && nchunks == 4)) && nchunks >= 2 && nchunks <= 4) {
+            const int cs = nchunks == 2 ? 2 : 4;
+            if (M <= (int64_t) device_cus() * (QD_WAVES / cs) * QK_RMAX) {
+                if (N == 1) {
+                    return cs == 2 ? launch_kslots<TYPE, 2, 1>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s)
+                                   : launch_kslots<TYPE, 4, 1>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+                }
+                return cs == 2 ? launch_kslots<TYPE, 2, 2>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s)
+                               : launch_kslots<TYPE, 4, 2>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
+            }
         }
     }
     if (dot_ok && N == 1) return launch_qmatvec_dot<TYPE, 1>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
