@@ -9,11 +9,19 @@
 //   sum_e (q_e*d + m) * x_e = d * sum_e q_e*x_e + m * sum_e x_e,
 // which reorders the reference's arithmetic; parity is by tolerance.
 //
-// Mapping: a wave owns R consecutive rows of W; its 64 lanes stride over the
-// row's blocks (lane l takes blocks l, l+64, ...). Each lane decodes one block
-// of each of the R rows once and reuses the decoded values for all N columns
-// of x, so x is read once per R rows. Partial sums are reduced across the wave
-// at the end and lane 0 writes the R x N outputs.
+// Kernels in this file (launch_type picks one per call):
+//   - k_qmatvec_dot: N = 1..4 on the packed integer dot instructions (below),
+//     weights through LDS when rows are 16-byte aligned;
+//   - k_qmatvec_kslots: the same arithmetic for one or two columns when K spans
+//     2..4 chunks of 4096 elements, one chunk per wave;
+//   - k_qmatvec_n1 / k_qmatvec: FP32 kernels for the shapes the integer-dot
+//     kernels do not take (odd block counts, misaligned x). In k_qmatvec a wave
+//     owns R consecutive rows of W and its 64 lanes stride over a row's blocks
+//     (lane l takes blocks l, l+64, ...); each lane decodes one block of each
+//     row once and reuses it for all N columns, and the partial sums are
+//     reduced across the wave at the end.
+// N from 4 (5 for the formats other than Q4_0) to 32 goes to the fp16 matrix-core
+// kernel in qmm.hip.
 #include "common.h"
 
 namespace trc_hip {
@@ -430,7 +438,7 @@ __global__ __launch_bounds__(QV1_WAVES * 64) void k_qmatvec_n1(const uint8_t* __
     }
 }
 
-// ---------------------------------------------------------------- N = 1, integer-dot kernel
+// ---------------------------------------------------------------- N = 1..4, integer-dot kernels
 //
 // The FP32 formulation costs about 2.4 VALU operations per weight element
 // (convert the nibble, multiply-add, unpack), which makes a batch-1 matvec
@@ -460,8 +468,9 @@ __global__ __launch_bounds__(QV1_WAVES * 64) void k_qmatvec_n1(const uint8_t* __
 //   - Each lane owns one pair of blocks of the chunk for every row its wave
 //     processes (pairs start on 4-byte boundaries for all formats). A wave
 //     handles at most QD_RMAX rows strided over all waves, with one or two
-//     rows of loads in flight; each row is reduced across the wave and stored
-//     as soon as its last chunk is done.
+//     rows of loads in flight; each row's part of a chunk is reduced across
+//     the wave as soon as it is computed and added into lane r, and the wave
+//     stores all its rows with one instruction after its last load.
 
 constexpr int QD_CH = 128;        // blocks per chunk of K (one lane = one pair)
 constexpr int QD_RMAX = 8;        // rows per wave at most
