@@ -97,6 +97,33 @@ constexpr bool rotated_even() {
 // A launch split over K adds two partial sums into y, so then (y0 != nullptr)
 // the wave also clears its share of column j of y: rows
 // [ch * per, (ch + 1) * per) with per = ceil(M / chunks).
+// Wave-wide reductions with DPP row operations (VALU latency, no LDS
+// round trips): within rows of 16, then into lane 63 with the row broadcasts,
+// whose masked-out rows keep 0 (the identity here: values are >= 0, flags 0/1).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int qm_dpp(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, ROW_MASK, 0xF, false);
+}
+__device__ __forceinline__ float qm_wave_max(float v) {  // every lane: max over the wave (v >= 0)
+    auto m = [](float a, int b) { return fmaxf(a, __builtin_bit_cast(float, b)); };
+    v = m(v, qm_dpp<0xB1, 0xF>(__builtin_bit_cast(int, v)));   // quad_perm [1,0,3,2]
+    v = m(v, qm_dpp<0x4E, 0xF>(__builtin_bit_cast(int, v)));   // quad_perm [2,3,0,1]
+    v = m(v, qm_dpp<0x141, 0xF>(__builtin_bit_cast(int, v)));  // row_half_mirror
+    v = m(v, qm_dpp<0x140, 0xF>(__builtin_bit_cast(int, v)));  // row_mirror
+    v = m(v, qm_dpp<0x142, 0xA>(__builtin_bit_cast(int, v)));  // row_bcast:15
+    v = m(v, qm_dpp<0x143, 0xC>(__builtin_bit_cast(int, v)));  // row_bcast:31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ int qm_wave_or(int v) {  // every lane: OR over the wave
+    v |= qm_dpp<0xB1, 0xF>(v);
+    v |= qm_dpp<0x4E, 0xF>(v);
+    v |= qm_dpp<0x141, 0xF>(v);
+    v |= qm_dpp<0x140, 0xF>(v);
+    v |= qm_dpp<0x142, 0xA>(v);
+    v |= qm_dpp<0x143, 0xC>(v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot,
                                                    int ncol, float* __restrict__ y0, int64_t ldy, int64_t M) {
     const int ch = blockIdx.x / ncol, j = blockIdx.x % ncol;  // columns past N get zeros
@@ -122,10 +149,8 @@ __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, i
         mx = fmaxf(mx, fabsf(v[k]));
         bad |= !__builtin_isfinite(v[k]);
     }
-    for (int o = 32; o > 0; o >>= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        bad |= __shfl_xor(bad, o, 64);
-    }
+    mx = qm_wave_max(mx);
+    bad = qm_wave_or(bad);
     const bool finite = bad == 0;
     // mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^QM_XBITS
     const int s = (mx > 0.f && finite) ? QM_XBITS - __builtin_amdgcn_frexp_expf(mx) : 0;
@@ -139,8 +164,9 @@ __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, i
         hi[k] = h;
         lo[k] = (_Float16) (e - (float) h);
     }
-    sm += __shfl_xor(sm, 1, 64);
-    sm += __shfl_xor(sm, 2, 64);
+    // the 4 lanes of a block (a quad): sum, in every one of them
+    sm += __builtin_bit_cast(float, qm_dpp<0xB1, 0xF>(__builtin_bit_cast(int, sm)));
+    sm += __builtin_bit_cast(float, qm_dpp<0x4E, 0xF>(__builtin_bit_cast(int, sm)));
     if (b < nblk) {
         uint4* dst = g_qm_a + ((int64_t) (j >> 4) * QM_MAX_BLOCKS + b) * 2 * 64 + (j & 15) + 16 * g;
         dst[0] = __builtin_bit_cast(uint4, hi);
