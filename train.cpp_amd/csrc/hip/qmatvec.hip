@@ -517,6 +517,18 @@ __device__ __forceinline__ void qd_load_x(const float* __restrict__ xc, int64_t 
 // (0 < U < 2^24) are D + 128, so the planes of U with each byte's top bit
 // flipped are the digits. Otherwise P0, P1 are the unsigned low bytes of X and
 // P2 its signed top byte (for the unsigned nibble quants and v_dot4_u32_u8).
+// Lane exchange inside a quad (DPP quad_perm; VALU latency, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float qd_quad_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int qd_quad_i(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+constexpr int QD_XOR1 = 0xB1;  // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int QD_XOR2 = 0x4E;  // quad_perm [2,3,0,1]: lane ^ 2
+
 // PS: LDS dwords per pair of planes (48, or QD_PSTRIDE with the padding that
 // makes the once-per-chunk 16-byte reads conflict-free).
 template <bool SIGNED, int PS = QD_PSTRIDE>
@@ -533,9 +545,9 @@ __device__ __forceinline__ void qd_prologue(const f4* v, int64_t cb, uint32_t* p
         bad |= !__builtin_isfinite(v[i].x) | !__builtin_isfinite(v[i].y) | !__builtin_isfinite(v[i].z) |
                !__builtin_isfinite(v[i].w);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    sm += __shfl_xor(sm, 1, 64);
-    bad |= __shfl_xor(bad, 1, 64);
+    mx = fmaxf(mx, qd_quad_f<QD_XOR1>(mx));
+    sm += qd_quad_f<QD_XOR1>(sm);
+    bad |= qd_quad_i<QD_XOR1>(bad);
     const bool finite = bad == 0;
     // s = 22 - E with mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^22
     const int s = (mx > 0.f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
@@ -630,12 +642,12 @@ __device__ __forceinline__ void qd_prologue_n4(const QdX4& x, int64_t cb, uint32
         sm += x.v[i].x + x.v[i].y;
         bad |= !__builtin_isfinite(x.v[i].x) | !__builtin_isfinite(x.v[i].y);
     }
-#pragma unroll
-    for (int m = 1; m <= 2; m <<= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-        sm += __shfl_xor(sm, m, 64);
-        bad |= __shfl_xor(bad, m, 64);
-    }
+    mx = fmaxf(mx, qd_quad_f<QD_XOR1>(mx));
+    sm += qd_quad_f<QD_XOR1>(sm);
+    bad |= qd_quad_i<QD_XOR1>(bad);
+    mx = fmaxf(mx, qd_quad_f<QD_XOR2>(mx));
+    sm += qd_quad_f<QD_XOR2>(sm);
+    bad |= qd_quad_i<QD_XOR2>(bad);
     const bool finite = bad == 0;
     // s = 22 - E with mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^22
     const int s = (mx > 0.f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
