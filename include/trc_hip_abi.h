@@ -149,12 +149,23 @@ int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b,
 
 /* Fused quantized matvec / skinny GEMM: y = mul_mat(W, x) with W quantized.
  *   W : `type` blocks, ne = [K, M]; row m starts at wq + m*nb1_w bytes
- *   x : F32, ne = [K, N]; column n starts at x + n*nb1_x bytes (x[k] contiguous)
- *   y : F32, ne = [M, N]; column n starts at y + n*nb1_y bytes (y[m] contiguous)
- * with K % 32 == 0 and 1 <= N <= TRC_HIP_QMATVEC_MAX_N; y must not overlap W or
- * x. The blocks are decoded in registers and never written out as F32. There is no counterpart in the
- * reference: its CPU path rejects quantized mul_mat (src/ops/trc_ops.cpp:368)
- * and the equivalent result is gguf_tensor_to_f32 followed by F32 mul_mat. */
+ *       (2-byte aligned rows; 4-byte for Q4_1/Q5_1)
+ *   x : F32, ne = [K, N]; column n starts at x + n*nb1_x bytes (x[k] contiguous;
+ *       x and nb1_x 16-byte aligned)
+ *   y : F32, ne = [M, N]; column n starts at y + n*nb1_y bytes (y[m] contiguous;
+ *       4-byte aligned)
+ * with K % 32 == 0 and 1 <= N <= TRC_HIP_QMATVEC_MAX_N. y must not share a byte
+ * with W or x (TRC_HIP_E_SHAPE otherwise). The blocks are decoded in registers
+ * and never written out as F32. There is no counterpart in the reference: its
+ * CPU path rejects quantized mul_mat (src/ops/trc_ops.cpp:368) and the
+ * equivalent result is gguf_tensor_to_f32 followed by F32 mul_mat.
+ * Streams: calls on different streams may overlap. For 2 <= N <= 32 (and the
+ * 32-column slices of wider N) x is converted into a device workspace of about
+ * 8.3 MiB that belongs to the (device, stream) pair: the first such call on a
+ * stream allocates it (hipMalloc; make that call before capturing the stream
+ * into a graph in global capture mode) and it is kept until the process ends.
+ * A captured graph keeps using the workspace of the stream it was captured on,
+ * so do not replay it concurrently with other work on that stream's workspace. */
 int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w,
                     const float* x, int64_t N, size_t nb1_x,
                     float* y, size_t nb1_y, void* stream);

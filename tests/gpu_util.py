@@ -2,6 +2,8 @@
 described to the C ABI as ggml tensors."""
 from __future__ import annotations
 
+import ctypes as C
+
 import numpy as np
 
 import oracle_lib as O
@@ -48,3 +50,26 @@ def gpu_mul_mat(a_dev: Dev, a_view, b_dev: Dev, b_view) -> np.ndarray:
     res = out.read()
     out.free()
     return res
+
+
+class Stream:
+    """A HIP stream of the runtime the library uses (hipStreamCreate/Destroy),
+    passed to the C ABI as its opaque handle."""
+
+    _rt = None
+
+    def __init__(self):
+        if Stream._rt is None:
+            rt = C.CDLL("libamdhip64.so")
+            rt.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+            rt.hipStreamDestroy.argtypes = [C.c_void_p]
+            Stream._rt = rt
+        h = C.c_void_p()
+        assert Stream._rt.hipStreamCreate(C.byref(h)) == 0
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            H.sync(self.handle)
+            assert Stream._rt.hipStreamDestroy(C.c_void_p(self.handle)) == 0
+            self.handle = None

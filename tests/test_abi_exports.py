@@ -70,6 +70,10 @@ def test_forced_error_hook_on_cpu():
     "H.check(H.load().trc_hip_dequant(2, None, -1, None, None))",
     "H.check(H.load().trc_hip_qmatvec(2, None, 48, 1, 27, None, 1, 192, None, 4, None))",
     "H.check(H.load().trc_hip_malloc(None, 16))",
+    # y overlapping W (rows of 36 bytes at 0x100000) or x (0x200000): refused
+    # before any device work, so the fake addresses are never dereferenced
+    "H.check(H.load().trc_hip_qmatvec(2, 0x100000, 64, 4, 36, 0x200000, 1, 256, 0x100040, 16, None))",
+    "H.check(H.load().trc_hip_qmatvec(2, 0x100000, 64, 4, 36, 0x200000, 2, 256, 0x2000f0, 16, None))",
 ])
 def test_argument_validation_precedes_device_work(bad):
     code = "import conftest\nfrom traincpp_amd import hip as H\ntry:\n    " + bad + \

@@ -9,7 +9,7 @@ import pytest
 
 import oracle_lib as O
 from conftest import announce
-from gpu_util import Dev, empty
+from gpu_util import Dev, Stream, empty
 from test_oracle_dequant import TYPES
 from traincpp_amd import hip as H
 from traincpp_amd import synth
@@ -255,3 +255,87 @@ def test_config2_q4_0_n64(hip):
     got = gpu_qmatvec(t, raw, K, M, X)
     want = oracle_qmatvec(t, raw, K, M, X)
     assert O.row_l2_error(got, want) <= TOL
+
+
+# Column contents for the dynamic-range cases of the integer-dot kernels (N = 1..4).
+def _range_column(p, K, rng):
+    x = rng.standard_normal(K).astype(np.float32)
+    if p == 0:
+        return np.full(K, 1e-41, np.float32) * np.sign(x)      # every element denormal
+    if p == 1:
+        return x * np.float32(1e-30)
+    if p == 2:
+        return x * np.float32(3e25)
+    if p == 3:
+        x[37] = np.float32(1e12)                                # an outlier inside a block
+        return x
+    if p == 4:
+        x[0:32] = np.float32(1e-40)                             # a denormal block beside normal ones
+        x[64:96] *= np.float32(1e-12)
+        return x
+    return x
+
+
+RANGE_PATTERNS = 6
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("N,p0", [(1, p) for p in range(RANGE_PATTERNS)] + [(2, 0), (2, 3), (3, 0), (3, 3),
+                                                                            (4, 0), (4, 2)])
+@pytest.mark.parametrize("K,M", [(4096, 96), (32 * 130, 96), (32 * 264, 160)])
+def test_dot_dynamic_range(hip, name, N, p0, K, M):
+    """The one- to four-column kernels scale x per 32-element block by a power
+    of two 2^-s that must stay a float down to all-denormal blocks: column j
+    holds pattern (p0 + j) % 6 (all-denormal, scale 1e-30, scale 3e25, a 1e12
+    outlier inside a block, a denormal block beside normal ones, unit). Weights
+    through LDS (K = 4096), through registers (130 blocks per row) and one chunk
+    per wave (264 blocks)."""
+    t = TYPES[name]
+    announce(f"qmatvec dot range {name} N={N} p0={p0} K={K}")
+    rng = np.random.default_rng(1000 * p0 + N + K)
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 50 + t + K))
+    X = np.stack([_range_column((p0 + j) % RANGE_PATTERNS, K, rng) for j in range(N)]).reshape(1, 1, N, K)
+    got = gpu_qmatvec(t, raw, K, M, X)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert np.isfinite(got).all()
+    assert O.row_l2_error(got, want) <= TOL
+    for j in range(N):
+        if (p0 + j) % RANGE_PATTERNS == 0:
+            # the bar's 1e-30 floor makes any tiny column pass, so the denormal
+            # column is also held to its own scale: the reference's products are
+            # themselves denormal and keep only a few bits, hence the loose 5 %
+            g, w = got[0, 0, j].astype(np.float64), want[0, 0, j].astype(np.float64)
+            assert np.abs(w).max() > 0
+            assert np.abs(g - w).max() <= 0.05 * np.abs(w).max()
+
+
+def test_two_streams_do_not_share_x(hip):
+    """Two different 16-column products (the matrix-core path, whose x planes go
+    to a device workspace) enqueued alternately on two streams, so that they
+    overlap on the GPU; each stream's calls must use its own workspace. Both
+    results match the oracle and equal, bit for bit, the same call run alone."""
+    t = TYPES["q4_0"]
+    K, M, N = 4096, 2048, 16
+    streams = [Stream(), Stream()]
+    cases = []
+    for c in range(2):
+        raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 900 + c))
+        X = synth.normal(910 + c, K * N).reshape(1, 1, N, K) * np.float32(10.0 ** (3 * c))
+        cases.append((raw, X, Dev(raw), Dev(X), empty((1, 1, N, M))))
+    announce("qmatvec two streams, 16 columns each")
+    for _ in range(40):
+        for c, (raw, X, dw, dx, dy) in enumerate(cases):
+            H.qmatvec(t, dw.ptr, K, M, (K // 32) * 18, dx.ptr, N, K * 4, dy.ptr, M * 4, streams[c].handle)
+    for s in streams:
+        H.sync(s.handle)
+    for c, (raw, X, dw, dx, dy) in enumerate(cases):
+        got = np.ascontiguousarray(dy.read())
+        assert O.row_l2_error(got, oracle_qmatvec(t, raw, K, M, X)) <= TOL
+        alone = empty((1, 1, N, M))
+        H.qmatvec(t, dw.ptr, K, M, (K // 32) * 18, dx.ptr, N, K * 4, alone.ptr, M * 4)
+        H.sync()
+        assert np.array_equal(got.view(np.uint32), np.ascontiguousarray(alone.read()).view(np.uint32))
+        for d in (dw, dx, dy, alone):
+            d.free()
+    for s in streams:
+        s.close()

@@ -342,8 +342,9 @@ private:
     }
 
     // mul_mat with a legacy quant src0: the fused kernel for skinny right-hand
-    // sides, otherwise the planes of src0 are dequantized into scratch and the
-    // FP32 MFMA kernel runs on them.
+    // sides whose columns meet its alignment (16-byte x columns, 4-byte y
+    // columns), otherwise the planes of src0 are dequantized into scratch and
+    // the FP32 MFMA kernel, which takes any 4-byte strides, runs on them.
     void mul_mat_quant(Tensor* t) {
         const Tensor* a = t->src[0];
         const Tensor* b = t->src[1];
@@ -351,7 +352,14 @@ private:
         uint8_t* pb = need_buffer(b)->address(b);
         uint8_t* pd = need_buffer(t)->address(t);
         const int64_t K = a->ne[0], M = a->ne[1], N = b->ne[1];
-        if (N <= TRC_HIP_QMATVEC_MAX_N) {
+        auto aligned = [](const uint8_t* p, const size_t* nb, const int64_t* ne, size_t al) {
+            if ((uintptr_t) p % al != 0) return false;
+            for (int i = 1; i < 4; ++i) {
+                if (ne[i] > 1 && nb[i] % al != 0) return false;
+            }
+            return true;
+        };
+        if (N <= TRC_HIP_QMATVEC_MAX_N && aligned(pb, b->nb, b->ne, 16) && aligned(pd, t->nb, t->ne, 4)) {
             for (int64_t i3 = 0; i3 < b->ne[3]; ++i3) {
                 for (int64_t i2 = 0; i2 < b->ne[2]; ++i2) {
                     const uint8_t* wa = pa + (i2 % a->ne[2]) * a->nb[2] + (i3 % a->ne[3]) * a->nb[3];

@@ -19,16 +19,6 @@ bool forced(const char* entry) {
     return v != nullptr && std::strcmp(v, entry) == 0;
 }
 
-int hip_status(hipError_t e, const char* what) {
-    if (e == hipSuccess) return TRC_HIP_OK;
-    std::snprintf(g_last_error, sizeof(g_last_error), "%s: %s (hipError_t %d)", what,
-                  hipGetErrorString(e), (int) e);
-    // The runtime also keeps the failure as its "last error"; clear it so that
-    // the launch check of a later kernel does not report this stale error.
-    (void) hipGetLastError();
-    return (int) e;
-}
-
 bool is_quant(int type) {
     return block_bytes(type) != 0;
 }
@@ -48,6 +38,16 @@ size_t basic_type_size(int type) {
 }
 }  // namespace
 
+int hip_error(hipError_t e, const char* what) {
+    if (e == hipSuccess) return TRC_HIP_OK;
+    std::snprintf(g_last_error, sizeof(g_last_error), "%s: %s (hipError_t %d)", what,
+                  hipGetErrorString(e), (int) e);
+    // The runtime also keeps the failure as its "last error"; clear it so that
+    // the launch check of a later kernel does not report this stale error.
+    (void) hipGetLastError();
+    return (int) e;
+}
+
 int fail(int code, const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
@@ -57,7 +57,7 @@ int fail(int code, const char* fmt, ...) {
 }
 
 int check_launch(const char* what) {
-    return hip_status(hipGetLastError(), what);
+    return hip_error(hipGetLastError(), what);
 }
 
 int device_cus() {
@@ -94,7 +94,7 @@ int trc_hip_device_count(int* count) {
     int n = 0;
     const hipError_t e = hipGetDeviceCount(&n);
     if (e == hipErrorNoDevice) return TRC_HIP_OK;
-    if (e != hipSuccess) return hip_status(e, "hipGetDeviceCount");
+    if (e != hipSuccess) return hip_error(e, "hipGetDeviceCount");
     *count = n;
     return TRC_HIP_OK;
 }
@@ -109,11 +109,11 @@ int trc_hip_init(int ordinal, trc_hip_props* props) {
     if (ordinal < 0 || ordinal >= n) {
         return fail(TRC_HIP_E_NO_DEVICE, "trc_hip_init: ordinal %d out of range (%d devices)", ordinal, n);
     }
-    int st = hip_status(hipSetDevice(ordinal), "hipSetDevice");
+    int st = hip_error(hipSetDevice(ordinal), "hipSetDevice");
     if (st != TRC_HIP_OK) return st;
     if (props == nullptr) return TRC_HIP_OK;
     hipDeviceProp_t p;
-    st = hip_status(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
+    st = hip_error(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
     if (st != TRC_HIP_OK) return st;
     std::memset(props, 0, sizeof(*props));
     std::snprintf(props->name, sizeof(props->name), "%s", p.name[0] ? p.name : "AMD GPU");
@@ -121,7 +121,7 @@ int trc_hip_init(int ordinal, trc_hip_props* props) {
     props->ordinal = ordinal;
     props->compute_units = p.multiProcessorCount;
     size_t free_b = 0, total_b = 0;
-    st = hip_status(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+    st = hip_error(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
     if (st != TRC_HIP_OK) return st;
     props->memory_free = free_b;
     props->memory_total = total_b;
@@ -132,7 +132,7 @@ int trc_hip_init(int ordinal, trc_hip_props* props) {
 
 int trc_hip_sync(void* stream) {
     TRC_FORCED("trc_hip_sync");
-    return hip_status(hipStreamSynchronize((hipStream_t) stream), "hipStreamSynchronize");
+    return hip_error(hipStreamSynchronize((hipStream_t) stream), "hipStreamSynchronize");
 }
 
 int trc_hip_malloc(void** ptr, size_t bytes) {
@@ -140,40 +140,40 @@ int trc_hip_malloc(void** ptr, size_t bytes) {
     *ptr = nullptr;
     TRC_FORCED("trc_hip_malloc");
     if (bytes == 0) return TRC_HIP_OK;
-    return hip_status(hipMalloc(ptr, bytes), "hipMalloc");
+    return hip_error(hipMalloc(ptr, bytes), "hipMalloc");
 }
 
 int trc_hip_free(void* ptr) {
     TRC_FORCED("trc_hip_free");
     if (ptr == nullptr) return TRC_HIP_OK;
-    return hip_status(hipFree(ptr), "hipFree");
+    return hip_error(hipFree(ptr), "hipFree");
 }
 
 int trc_hip_h2d(void* dst, const void* src, size_t bytes, void* stream) {
     TRC_FORCED("trc_hip_h2d");
     if (bytes == 0) return TRC_HIP_OK;
     if (dst == nullptr || src == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_h2d: NULL pointer");
-    int st = hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t) stream),
-                        "hipMemcpyAsync(H2D)");
+    int st = hip_error(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t) stream),
+                       "hipMemcpyAsync(H2D)");
     if (st != TRC_HIP_OK) return st;
-    return hip_status(hipStreamSynchronize((hipStream_t) stream), "hipStreamSynchronize(H2D)");
+    return hip_error(hipStreamSynchronize((hipStream_t) stream), "hipStreamSynchronize(H2D)");
 }
 
 int trc_hip_d2h(void* dst, const void* src, size_t bytes, void* stream) {
     TRC_FORCED("trc_hip_d2h");
     if (bytes == 0) return TRC_HIP_OK;
     if (dst == nullptr || src == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_d2h: NULL pointer");
-    int st = hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t) stream),
-                        "hipMemcpyAsync(D2H)");
+    int st = hip_error(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t) stream),
+                       "hipMemcpyAsync(D2H)");
     if (st != TRC_HIP_OK) return st;
-    return hip_status(hipStreamSynchronize((hipStream_t) stream), "hipStreamSynchronize(D2H)");
+    return hip_error(hipStreamSynchronize((hipStream_t) stream), "hipStreamSynchronize(D2H)");
 }
 
 int trc_hip_memset(void* dst, int value, size_t bytes, void* stream) {
     TRC_FORCED("trc_hip_memset");
     if (bytes == 0) return TRC_HIP_OK;
     if (dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_memset: NULL pointer");
-    return hip_status(hipMemsetAsync(dst, value, bytes, (hipStream_t) stream), "hipMemsetAsync");
+    return hip_error(hipMemsetAsync(dst, value, bytes, (hipStream_t) stream), "hipMemsetAsync");
 }
 
 int trc_hip_fill_f32(float* dst, float value, int64_t count, void* stream) {
@@ -254,6 +254,14 @@ int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w
     if (nb1_w < row_bytes && M > 1) return fail(TRC_HIP_E_SHAPE, "trc_hip_qmatvec: nb1_w %zu < row size %zu", nb1_w, row_bytes);
     if ((N > 1 && (nb1_x < (size_t) K * 4 || nb1_y < (size_t) M * 4))) {
         return fail(TRC_HIP_E_SHAPE, "trc_hip_qmatvec: columns of x or y overlap");
+    }
+    // y is written (and, for some shapes, cleared first) while W and x are read,
+    // so it must share no byte with either (compared by the spans they cover)
+    const uintptr_t w0 = (uintptr_t) wq, w1 = w0 + (uintptr_t) (M - 1) * nb1_w + row_bytes;
+    const uintptr_t x0 = (uintptr_t) x, x1 = x0 + (uintptr_t) (N - 1) * nb1_x + (uintptr_t) K * 4;
+    const uintptr_t y0 = (uintptr_t) y, y1 = y0 + (uintptr_t) (N - 1) * nb1_y + (uintptr_t) M * 4;
+    if ((y0 < w1 && w0 < y1) || (y0 < x1 && x0 < y1)) {
+        return fail(TRC_HIP_E_SHAPE, "trc_hip_qmatvec: y overlaps W or x");
     }
     return launch_qmatvec(type, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, (hipStream_t) stream);
 }

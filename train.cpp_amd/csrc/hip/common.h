@@ -36,6 +36,8 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
 // Launch-side error reporting, implemented in abi.hip.
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// hipSuccess -> TRC_HIP_OK; otherwise records "what: <HIP message>" and returns e.
+int hip_error(hipError_t e, const char* what);
 // Compute units of the current device (cached per device).
 int device_cus();
 
@@ -48,10 +50,14 @@ int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w,
                    int64_t N, size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream);
 // Fused quant x skinny GEMM on the fp16 matrix cores for 2 <= N <= 32 (N = 2, 3
 // only off the integer-dot kernel's alignment)
-// (qmm.hip); qmm_supported says whether the shape and alignment fit it.
+// (qmm.hip); qmm_supported says whether the shape and alignment fit it. Its x
+// planes and scales go to a device workspace per (device, stream), allocated
+// by the first such call on that stream (qm_stream_workspace).
 bool qmm_supported(int64_t K, int64_t N, const void* wq, size_t nb1_w);
 int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
                size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream);
+size_t qm_workspace_bytes();
+int qm_stream_workspace(hipStream_t stream, uint8_t** ws);
 int launch_add_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t stream);
 int launch_acc_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, size_t nb1, size_t nb2,
                    size_t nb3, size_t offset, int inplace, hipStream_t stream);

@@ -549,8 +549,10 @@ __device__ __forceinline__ void qd_prologue(const f4* v, int64_t cb, uint32_t* p
     sm += qd_quad_f<QD_XOR1>(sm);
     bad |= qd_quad_i<QD_XOR1>(bad);
     const bool finite = bad == 0;
-    // s = 22 - E with mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^22
-    const int s = (mx > 0.f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
+    // s = 22 - E with mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^22. At most
+    // 149, so that 2^-s stays a float: below 2^-127 every x is a multiple of 2^-149,
+    // and x * 2^149 is then an exact integer under 2^22.
+    const int s = (mx > 0.f && finite) ? min(22 - __builtin_amdgcn_frexp_expf(mx), 149) : 0;
     uint32_t P[3][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -649,8 +651,10 @@ __device__ __forceinline__ void qd_prologue_n4(const QdX4& x, int64_t cb, uint32
     sm += qd_quad_f<QD_XOR2>(sm);
     bad |= qd_quad_i<QD_XOR2>(bad);
     const bool finite = bad == 0;
-    // s = 22 - E with mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^22
-    const int s = (mx > 0.f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
+    // s = 22 - E with mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^22. At most
+    // 149, so that 2^-s stays a float: below 2^-127 every x is a multiple of 2^-149,
+    // and x * 2^149 is then an exact integer under 2^22.
+    const int s = (mx > 0.f && finite) ? min(22 - __builtin_amdgcn_frexp_expf(mx), 149) : 0;
     uint32_t U[8];  // low elements 0-3, high elements 4-7
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -710,8 +714,9 @@ __device__ __forceinline__ float qd_block(const uint32_t* q, uint32_t qh, uint32
     s0 += t0;
     s1 += t1;
     s2 += t2;
-    // sum_e q_e X_e = s0 + 256 s1 + 65536 s2 (s0 + 256 s1 < 2^25)
-    const float qx = __builtin_fmaf((float) s2, 65536.f, (float) (s0 + (s1 << 8))) * scale;
+    // sum_e q_e X_e = s0 + 256 s1 + 65536 s2. s0 and s1 stay under 32 * 31 * 255 < 2^18,
+    // so both convert exactly and s0 + 256 s1 rounds once, in the first fma.
+    const float qx = __builtin_fmaf((float) s2, 65536.f, __builtin_fmaf((float) s1, 256.f, (float) s0)) * scale;
     const float d = half_bits_to_float(d_bits);
     if constexpr (TYPE == TRC_HIP_TYPE_Q4_0) return d * __builtin_fmaf(-8.f, xs, qx);
     if constexpr (TYPE == TRC_HIP_TYPE_Q5_0) return d * __builtin_fmaf(-16.f, xs, qx);
@@ -1416,7 +1421,7 @@ int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w,
     if (N > 16 && !(N <= 32 && qmm_supported(K, N, wq, nb1_w))) {
         // skinny GEMM beyond the columns one launch carries: one fused pass over W
         // per 32 columns on the matrix-core kernel, else per 16 (the launches run
-        // in order on the stream, so they can share the x scratch)
+        // in order on the stream, so they can share the x workspace)
         const int64_t step = qmm_supported(K, 32, wq, nb1_w) ? 32 : 16;
         for (int64_t c0 = 0; c0 < N; c0 += step) {
             const int64_t n = N - c0 < step ? N - c0 : step;

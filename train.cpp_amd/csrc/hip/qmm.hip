@@ -73,14 +73,16 @@ constexpr int QM_COLS = 16 * QM_NT;    // columns per chunk and block in the x m
 constexpr int QM_META_XS = QM_MAX_BLOCKS / QM_CHB * QM_COLS;  // block sums follow the chunk scales
 constexpr uint32_t QM_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
 
-// x in fp16 planes, written by k_qmm_xprep and read by k_qmm on the same stream.
-// A operands: [column tile u][block][plane hi, lo][lane 0..63] 16 bytes each
-// (tile u holds columns 16u .. 16u + 15). Meta: 2^-s per (chunk, column j) (f32,
-// NaN for a chunk with a non-finite value) at [chunk * QM_COLS + j], then the
-// block sums of x' = x * 2^s at [QM_META_XS + block * QM_COLS + j] (read for
-// Q4_1/Q5_1). Calls that overlap on one GPU race.
-__device__ __attribute__((aligned(256))) uint4 g_qm_a[QM_NT * QM_MAX_BLOCKS * 2 * 64];
-__device__ __attribute__((aligned(256))) float g_qm_meta[QM_META_XS + QM_MAX_BLOCKS * QM_COLS];
+// x in fp16 planes, written by k_qmm_xprep and read by k_qmm on the same stream,
+// in a workspace of QM_WS_BYTES: the A operands, [column tile u][block][plane hi,
+// lo][lane 0..63] 16 bytes each (tile u holds columns 16u .. 16u + 15), then the
+// meta floats: 2^-s per (chunk, column j) (NaN for a chunk with a non-finite
+// value) at [chunk * QM_COLS + j], then the block sums of x' = x * 2^s at
+// [QM_META_XS + block * QM_COLS + j] (read for Q4_1/Q5_1). k_qmm_xprep writes
+// every entry k_qmm reads, so a workspace needs no clearing between calls.
+constexpr int QM_A_BYTES = QM_NT * QM_MAX_BLOCKS * 2 * 64 * 16;
+constexpr int QM_META_BYTES = (QM_META_XS + QM_MAX_BLOCKS * QM_COLS) * 4;
+static_assert(QM_A_BYTES % 256 == 0, "the meta floats start 256-byte aligned");
 
 template <int TYPE>
 constexpr bool rotated_even() {
@@ -125,7 +127,10 @@ __device__ __forceinline__ int qm_wave_or(int v) {  // every lane: OR over the w
 }
 
 __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot,
-                                                   int ncol, float* __restrict__ y0, int64_t ldy, int64_t M) {
+                                                   int ncol, float* __restrict__ y0, int64_t ldy, int64_t M,
+                                                   uint8_t* __restrict__ ws) {
+    uint4* const xa = (uint4*) ws;
+    float* const meta = (float*) (ws + QM_A_BYTES);
     const int ch = blockIdx.x / ncol, j = blockIdx.x % ncol;  // columns past N get zeros
     const int l = threadIdx.x, bl = l >> 2, g = l & 3;
     if (y0 != nullptr && j < N) {
@@ -152,8 +157,10 @@ __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, i
     mx = qm_wave_max(mx);
     bad = qm_wave_or(bad);
     const bool finite = bad == 0;
-    // mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^QM_XBITS
-    const int s = (mx > 0.f && finite) ? QM_XBITS - __builtin_amdgcn_frexp_expf(mx) : 0;
+    // mx = f * 2^E, f in [0.5, 1): every |x| * 2^s < 2^QM_XBITS. At most 149, so that
+    // 2^-s stays a float: below 2^-135 every x is a multiple of 2^-149, and
+    // x * 2^149 is then an exact integer under 2^14.
+    const int s = (mx > 0.f && finite) ? min(QM_XBITS - __builtin_amdgcn_frexp_expf(mx), 149) : 0;
     h8 hi, lo;
     float sm = 0.f;
 #pragma unroll
@@ -168,12 +175,12 @@ __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, i
     sm += __builtin_bit_cast(float, qm_dpp<0xB1, 0xF>(__builtin_bit_cast(int, sm)));
     sm += __builtin_bit_cast(float, qm_dpp<0x4E, 0xF>(__builtin_bit_cast(int, sm)));
     if (b < nblk) {
-        uint4* dst = g_qm_a + ((int64_t) (j >> 4) * QM_MAX_BLOCKS + b) * 2 * 64 + (j & 15) + 16 * g;
+        uint4* dst = xa + ((int64_t) (j >> 4) * QM_MAX_BLOCKS + b) * 2 * 64 + (j & 15) + 16 * g;
         dst[0] = __builtin_bit_cast(uint4, hi);
         dst[64] = __builtin_bit_cast(uint4, lo);
-        if (g == 0) g_qm_meta[QM_META_XS + b * QM_COLS + j] = sm;
+        if (g == 0) meta[QM_META_XS + b * QM_COLS + j] = sm;
     }
-    if (l == 0) g_qm_meta[ch * QM_COLS + j] = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
+    if (l == 0) meta[ch * QM_COLS + j] = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
 }
 
 // Per format: which dwords of a pair each lane loads (NW of them), in bytes
@@ -475,7 +482,8 @@ struct QmTile {
 template <int TYPE, int T, int ROUNDS, int R, int NT>
 __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict__ W, int nblk, int64_t M,
                                                         int64_t nb1_w, float* __restrict__ y, int64_t ldy, int N,
-                                                        int rows_per_wg, int part_chunks) {
+                                                        int rows_per_wg, int part_chunks,
+                                                        const uint8_t* __restrict__ ws) {
     using TL = QmTile<TYPE, T, ROUNDS>;
     constexpr int NW = QmFmt<TYPE>::NW, PW = TL::PW;
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
@@ -502,10 +510,10 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     // The workgroup's rows as one buffer (the launcher keeps it below 2^31 bytes).
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         (void*) (W + r0 * nb1_w), (short) 0, (int) ((int64_t) rows * nb1_w), QM_RSRC_WORD3);
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-        (void*) g_qm_a, (short) 0, (int) sizeof(g_qm_a), QM_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*) ws, (short) 0, QM_A_BYTES, QM_RSRC_WORD3);
     const __amdgpu_buffer_rsrc_t rm =
-        __builtin_amdgcn_make_buffer_rsrc((void*) g_qm_meta, (short) 0, (int) sizeof(g_qm_meta), QM_RSRC_WORD3);
+        __builtin_amdgcn_make_buffer_rsrc((void*) (ws + QM_A_BYTES), (short) 0, QM_META_BYTES, QM_RSRC_WORD3);
 
     // LDS slot k * 512 + thread = row q / LS16, piece q % LS16 of a chunk: rows
     // sit TL::LS = RB + 16 bytes apart, an odd number of 16-byte pieces, so the
@@ -627,11 +635,11 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
 
 template <int TYPE, int T, int ROUNDS, int R, int NT>
 int launch_t(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows, int parts,
-             int part_chunks, hipStream_t s) {
+             int part_chunks, const uint8_t* ws, hipStream_t s) {
     const int64_t grid = (M + rows - 1) / rows;
     hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R, NT>), dim3((unsigned) grid, (unsigned) parts), dim3(QM_WAVES * 64), 0,
                        s, (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, y, (int64_t) (nb1_y / sizeof(float)), N, rows,
-                       part_chunks);
+                       part_chunks, ws);
     return check_launch("qmm");
 }
 
@@ -675,17 +683,17 @@ constexpr int qm_max_rows() {
 // two values.
 template <int TYPE, int T, int NT>
 int launch_rounds(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
-                  int parts, int part_chunks, hipStream_t s) {
+                  int parts, int part_chunks, const uint8_t* ws, hipStream_t s) {
     constexpr int LS16 = qm_ls16<TYPE>();
     constexpr int LO = qm_rounds(16 * T - 8, LS16), HI = qm_rounds(16 * T, LS16);
     const int rounds = qm_rounds(rows, LS16);
     if (rounds <= LO) {
         return launch_t<TYPE, T, LO, qm_ring<TYPE, NT>(T, LO), NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
-                                                               part_chunks, s);
+                                                               part_chunks, ws, s);
     }
     if constexpr (16 * T <= qm_max_rows<TYPE, NT>()) {  // 16T rows is within the cap
         return launch_t<TYPE, T, HI, qm_ring<TYPE, NT>(T, HI), NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
-                                                               part_chunks, s);
+                                                               part_chunks, ws, s);
     } else {
         return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
     }
@@ -693,12 +701,12 @@ int launch_rounds(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, s
 
 template <int TYPE, int T, int NT>
 int launch_tiles(int t, const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
-                 int parts, int part_chunks, hipStream_t s) {
+                 int parts, int part_chunks, const uint8_t* ws, hipStream_t s) {
     if constexpr (T > (qm_max_rows<TYPE, NT>() + 15) / 16) {
         return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
     } else {
-        if (t == T) return launch_rounds<TYPE, T, NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, s);
-        return launch_tiles<TYPE, T + 1, NT>(t, wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, s);
+        if (t == T) return launch_rounds<TYPE, T, NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, ws, s);
+        return launch_tiles<TYPE, T + 1, NT>(t, wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, ws, s);
     }
 }
 
@@ -729,23 +737,23 @@ QmPlan qm_plan(int nblk, int64_t M) {
 // NT = 1 for N <= 16, 2 for 17 <= N <= 32: every column tile shares one pass over W.
 template <int TYPE, int NT>
 int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
-               size_t nb1_y, hipStream_t s) {
+               size_t nb1_y, uint8_t* ws, hipStream_t s) {
     const QmPlan p = qm_plan<TYPE, NT>(nblk, M);
     const int nchunks = (nblk + QM_CHB - 1) / QM_CHB;
     hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) (nchunks * 16 * NT)), dim3(64), 0, s, x,
                        (int64_t) (nb1_x / sizeof(float)), N, nblk, rotated_even<TYPE>() ? 2 : 0, 16 * NT,
-                       p.parts > 1 ? y : nullptr, (int64_t) (nb1_y / sizeof(float)), M);
+                       p.parts > 1 ? y : nullptr, (int64_t) (nb1_y / sizeof(float)), M, ws);
     const int rc = check_launch("qmm_xprep");
     if (rc != TRC_HIP_OK) return rc;
     return launch_tiles<TYPE, 1, NT>((p.rows + 15) / 16, wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts,
-                                     p.part_chunks, s);
+                                     p.part_chunks, ws, s);
 }
 
 template <int TYPE>
 int launch_cols(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
-                size_t nb1_y, hipStream_t s) {
-    if (N > 16) return launch_fmt<TYPE, 2>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, s);
-    return launch_fmt<TYPE, 1>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, s);
+                size_t nb1_y, uint8_t* ws, hipStream_t s) {
+    if (N > 16) return launch_fmt<TYPE, 2>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
+    return launch_fmt<TYPE, 1>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
 }
 
 }  // namespace
@@ -762,14 +770,77 @@ bool qmm_supported(int64_t K, int64_t N, const void* wq, size_t nb1_w) {
 int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
                size_t nb1_x, float* y, size_t nb1_y, hipStream_t s) {
     const int nblk = (int) (K / QK);
+    if (nblk > QM_MAX_BLOCKS) {
+        return fail(TRC_HIP_E_SHAPE, "qmm: K = %lld exceeds the %d the x workspace holds", (long long) K,
+                    QM_MAX_BLOCKS * QK);
+    }
+    uint8_t* ws = nullptr;
+    const int rc = qm_stream_workspace(s, &ws);
+    if (rc != TRC_HIP_OK) return rc;
     switch (type) {
-        case TRC_HIP_TYPE_Q4_0: return launch_cols<TRC_HIP_TYPE_Q4_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
-        case TRC_HIP_TYPE_Q4_1: return launch_cols<TRC_HIP_TYPE_Q4_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
-        case TRC_HIP_TYPE_Q5_0: return launch_cols<TRC_HIP_TYPE_Q5_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
-        case TRC_HIP_TYPE_Q5_1: return launch_cols<TRC_HIP_TYPE_Q5_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
-        case TRC_HIP_TYPE_Q8_0: return launch_cols<TRC_HIP_TYPE_Q8_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, s);
+        case TRC_HIP_TYPE_Q4_0: return launch_cols<TRC_HIP_TYPE_Q4_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
+        case TRC_HIP_TYPE_Q4_1: return launch_cols<TRC_HIP_TYPE_Q4_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
+        case TRC_HIP_TYPE_Q5_0: return launch_cols<TRC_HIP_TYPE_Q5_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
+        case TRC_HIP_TYPE_Q5_1: return launch_cols<TRC_HIP_TYPE_Q5_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
+        case TRC_HIP_TYPE_Q8_0: return launch_cols<TRC_HIP_TYPE_Q8_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
         default: return fail(TRC_HIP_E_INVALID, "qmm: bad type %d", type);
     }
+}
+
+}  // namespace trc_hip
+
+// ---------------------------------------------------------------- x workspaces
+//
+// One workspace per (device, stream), allocated by the first call on that
+// stream that takes this path and kept until the process ends. Work on one
+// stream runs in order, so calls on different streams never share x planes.
+// hipStreamPerThread names a different stream in every host thread, so its
+// workspaces are also keyed by thread.
+#include <mutex>
+#include <thread>
+#include <vector>
+
+namespace trc_hip {
+namespace {
+
+constexpr size_t QM_WS_BYTES = (size_t) QM_A_BYTES + (size_t) QM_META_BYTES;
+std::mutex g_ws_mutex;
+
+struct StreamWs {
+    int dev;
+    hipStream_t stream;
+    std::thread::id thread;  // only for hipStreamPerThread
+    uint8_t* ptr;
+};
+std::vector<StreamWs>& stream_workspaces() {
+    static std::vector<StreamWs> v;
+    return v;
+}
+
+}  // namespace
+
+size_t qm_workspace_bytes() {
+    return QM_WS_BYTES;
+}
+
+int qm_stream_workspace(hipStream_t s, uint8_t** ws) {
+    int dev = 0;
+    const hipError_t ge = hipGetDevice(&dev);
+    if (ge != hipSuccess) return hip_error(ge, "hipGetDevice");
+    const std::thread::id tid = s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    for (const StreamWs& w : stream_workspaces()) {
+        if (w.dev == dev && w.stream == s && w.thread == tid) {
+            *ws = w.ptr;
+            return TRC_HIP_OK;
+        }
+    }
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, QM_WS_BYTES);
+    if (e != hipSuccess) return hip_error(e, "qmatvec: x workspace for a new stream (hipMalloc)");
+    stream_workspaces().push_back({dev, s, tid, (uint8_t*) p});
+    *ws = (uint8_t*) p;
+    return TRC_HIP_OK;
 }
 
 }  // namespace trc_hip
