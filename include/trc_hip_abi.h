@@ -170,6 +170,21 @@ int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w
                     const float* x, int64_t N, size_t nb1_x,
                     float* y, size_t nb1_y, void* stream);
 
+/* trc_hip_qmatvec without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. Same arguments,
+ * results (bit for bit) and errors as trc_hip_qmatvec. Where trc_hip_qmatvec
+ * converts x into its per-stream workspace, this entry uses instead one fixed
+ * device array of about 8.3 MiB (the x planes of 32 columns of up to 65536
+ * elements, the most any call converts), which each GPU holds from library
+ * load until the process ends. Every call of this entry on one GPU shares that
+ * array, so calls that overlap on one GPU (on different streams, or in graphs
+ * replayed concurrently) race; serialise them. Nothing in it needs clearing
+ * between calls. */
+int trc_hip_qmatvec_noalloc(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w,
+                            const float* x, int64_t N, size_t nb1_x,
+                            float* y, size_t nb1_y, void* stream);
+
 /* Strided copy between two tensors of the same type and shape, in ggml linear
  * element order (OP_DUP/OP_CPY/OP_CONT: src/ops/trc_ops.cpp:124-134, computed by
  * compute_dup src/backends/cpu/trc_cpu_ops.cpp:219-236). Element size 1, 2, 4 or 8 B. */

@@ -111,6 +111,9 @@ int trc_hip_init(int ordinal, trc_hip_props* props) {
     }
     int st = hip_error(hipSetDevice(ordinal), "hipSetDevice");
     if (st != TRC_HIP_OK) return st;
+    // the address of trc_hip_qmatvec_noalloc's fixed workspace on this device
+    st = qm_scratch_setup();
+    if (st != TRC_HIP_OK) return st;
     if (props == nullptr) return TRC_HIP_OK;
     hipDeviceProp_t p;
     st = hip_error(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
@@ -238,22 +241,26 @@ int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const 
     return launch_mul_mat_f32(*a, *b, *dst, (hipStream_t) stream);
 }
 
-int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
-                    size_t nb1_x, float* y, size_t nb1_y, void* stream) {
-    TRC_FORCED("trc_hip_qmatvec");
-    if (!is_quant(type)) return fail(TRC_HIP_E_INVALID, "trc_hip_qmatvec: type %d is not a legacy quant type", type);
+}  // extern "C"
+
+namespace {
+
+// Argument checks shared by trc_hip_qmatvec and trc_hip_qmatvec_noalloc.
+int qmatvec_args(const char* entry, int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x,
+                 int64_t N, size_t nb1_x, const float* y, size_t nb1_y) {
+    if (!is_quant(type)) return fail(TRC_HIP_E_INVALID, "%s: type %d is not a legacy quant type", entry, type);
     if (K <= 0 || M <= 0 || N <= 0 || K % QK != 0) {
-        return fail(TRC_HIP_E_SHAPE, "trc_hip_qmatvec: need K > 0, K %% 32 == 0, M > 0, N > 0 (K=%lld M=%lld N=%lld)",
+        return fail(TRC_HIP_E_SHAPE, "%s: need K > 0, K %% 32 == 0, M > 0, N > 0 (K=%lld M=%lld N=%lld)", entry,
                     (long long) K, (long long) M, (long long) N);
     }
     if (N > TRC_HIP_QMATVEC_MAX_N) {
-        return fail(TRC_HIP_E_SHAPE, "trc_hip_qmatvec: N=%lld exceeds %d", (long long) N, TRC_HIP_QMATVEC_MAX_N);
+        return fail(TRC_HIP_E_SHAPE, "%s: N=%lld exceeds %d", entry, (long long) N, TRC_HIP_QMATVEC_MAX_N);
     }
-    if (wq == nullptr || x == nullptr || y == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_qmatvec: NULL pointer");
+    if (wq == nullptr || x == nullptr || y == nullptr) return fail(TRC_HIP_E_INVALID, "%s: NULL pointer", entry);
     const size_t row_bytes = (size_t) (K / QK) * (size_t) block_bytes(type);
-    if (nb1_w < row_bytes && M > 1) return fail(TRC_HIP_E_SHAPE, "trc_hip_qmatvec: nb1_w %zu < row size %zu", nb1_w, row_bytes);
+    if (nb1_w < row_bytes && M > 1) return fail(TRC_HIP_E_SHAPE, "%s: nb1_w %zu < row size %zu", entry, nb1_w, row_bytes);
     if ((N > 1 && (nb1_x < (size_t) K * 4 || nb1_y < (size_t) M * 4))) {
-        return fail(TRC_HIP_E_SHAPE, "trc_hip_qmatvec: columns of x or y overlap");
+        return fail(TRC_HIP_E_SHAPE, "%s: columns of x or y overlap", entry);
     }
     // y is written (and, for some shapes, cleared first) while W and x are read,
     // so it must share no byte with either (compared by the spans they cover)
@@ -261,9 +268,29 @@ int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w
     const uintptr_t x0 = (uintptr_t) x, x1 = x0 + (uintptr_t) (N - 1) * nb1_x + (uintptr_t) K * 4;
     const uintptr_t y0 = (uintptr_t) y, y1 = y0 + (uintptr_t) (N - 1) * nb1_y + (uintptr_t) M * 4;
     if ((y0 < w1 && w0 < y1) || (y0 < x1 && x0 < y1)) {
-        return fail(TRC_HIP_E_SHAPE, "trc_hip_qmatvec: y overlaps W or x");
+        return fail(TRC_HIP_E_SHAPE, "%s: y overlaps W or x", entry);
     }
-    return launch_qmatvec(type, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, (hipStream_t) stream);
+    return TRC_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
+                    size_t nb1_x, float* y, size_t nb1_y, void* stream) {
+    TRC_FORCED("trc_hip_qmatvec");
+    const int rc = qmatvec_args("trc_hip_qmatvec", type, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y);
+    if (rc != TRC_HIP_OK) return rc;
+    return launch_qmatvec(type, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, (hipStream_t) stream, QmScratch::PER_STREAM);
+}
+
+int trc_hip_qmatvec_noalloc(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
+                            size_t nb1_x, float* y, size_t nb1_y, void* stream) {
+    TRC_FORCED("trc_hip_qmatvec_noalloc");
+    const int rc = qmatvec_args("trc_hip_qmatvec_noalloc", type, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y);
+    if (rc != TRC_HIP_OK) return rc;
+    return launch_qmatvec(type, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, (hipStream_t) stream, QmScratch::STATIC);
 }
 
 int trc_hip_cpy(const trc_hip_tensor* src, const trc_hip_tensor* dst, void* stream) {

@@ -46,17 +46,25 @@ int device_cus();
 int launch_dequant(int type, const void* blocks, int64_t n_blocks, float* dst, hipStream_t stream);
 int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d,
                        hipStream_t stream);
+// Where the fp16 matrix-core path of the fused matvec keeps x's planes and
+// scales (qmm.hip): a workspace per (device, stream), allocated by the first
+// such call on that stream (trc_hip_qmatvec), or the fixed device array of the
+// current GPU (trc_hip_qmatvec_noalloc: no allocation, shared by every such call
+// on that GPU).
+enum class QmScratch { PER_STREAM, STATIC };
 int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x,
-                   int64_t N, size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream);
+                   int64_t N, size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream, QmScratch where);
 // Fused quant x skinny GEMM on the fp16 matrix cores for 2 <= N <= 32 (N = 2, 3
 // only off the integer-dot kernel's alignment)
-// (qmm.hip); qmm_supported says whether the shape and alignment fit it. Its x
-// planes and scales go to a device workspace per (device, stream), allocated
-// by the first such call on that stream (qm_stream_workspace).
+// (qmm.hip); qmm_supported says whether the shape and alignment fit it.
 bool qmm_supported(int64_t K, int64_t N, const void* wq, size_t nb1_w);
 int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
-               size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream);
+               size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream, QmScratch where);
+// The x workspaces (qmm.hip). qm_scratch_setup finds the address of the fixed
+// array on the current device (once per device; it allocates nothing).
 size_t qm_workspace_bytes();
+int qm_scratch_setup();
+int qm_static_scratch(uint8_t** ws);
 int qm_stream_workspace(hipStream_t stream, uint8_t** ws);
 int launch_add_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t stream);
 int launch_acc_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, size_t nb1, size_t nb2,

@@ -1355,7 +1355,7 @@ int launch_nb(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x
 
 template <int TYPE>
 int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N, size_t nb1_x,
-                float* y, size_t nb1_y, hipStream_t s) {
+                float* y, size_t nb1_y, hipStream_t s, QmScratch where) {
     const int64_t nblk = K / QK;
     // N = 1..4: integer-dot kernel (one pass over W for all columns; each
     // column's digit planes take 48 registers, so a third and fourth column fit
@@ -1398,7 +1398,7 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
         return launch_qmatvec_dot<TYPE, 4>(wq, nblk, M, nb1_w, x, nb1_x, y, nb1_y, s);
     }
     // 3 <= N <= 32 (and N = 2 off the dot kernel's alignment): fp16 matrix-core kernel (qmm.hip)
-    if (qmm_supported(K, N, wq, nb1_w)) return launch_qmm(TYPE, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s);
+    if (qmm_supported(K, N, wq, nb1_w)) return launch_qmm(TYPE, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, s, where);
     // N = 1 streaming kernel: needs 16-byte aligned rows and row chunks
     if (N == 1 && nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0) {
         // Q8_0 blocks are twice as large: a 4-row tile already fills the registers.
@@ -1417,7 +1417,7 @@ int launch_type(const void* wq, int64_t K, int64_t M, size_t nb1_w, const float*
 }  // namespace
 
 int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
-                   size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream) {
+                   size_t nb1_x, float* y, size_t nb1_y, hipStream_t stream, QmScratch where) {
     if (N > 16 && !(N <= 32 && qmm_supported(K, N, wq, nb1_w))) {
         // skinny GEMM beyond the columns one launch carries: one fused pass over W
         // per 32 columns on the matrix-core kernel, else per 16 (the launches run
@@ -1426,7 +1426,7 @@ int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w,
         for (int64_t c0 = 0; c0 < N; c0 += step) {
             const int64_t n = N - c0 < step ? N - c0 : step;
             const int rc = launch_qmatvec(type, wq, K, M, nb1_w, (const float*) ((const uint8_t*) x + c0 * nb1_x), n,
-                                          nb1_x, (float*) ((uint8_t*) y + c0 * nb1_y), nb1_y, stream);
+                                          nb1_x, (float*) ((uint8_t*) y + c0 * nb1_y), nb1_y, stream, where);
             if (rc != TRC_HIP_OK) return rc;
         }
         return TRC_HIP_OK;
@@ -1440,11 +1440,11 @@ int launch_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w,
         return fail(TRC_HIP_E_ALIGN, "qmatvec: x columns must be 16-byte and y columns 4-byte aligned");
     }
     switch (type) {
-        case TRC_HIP_TYPE_Q4_0: return launch_type<TRC_HIP_TYPE_Q4_0>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream);
-        case TRC_HIP_TYPE_Q4_1: return launch_type<TRC_HIP_TYPE_Q4_1>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream);
-        case TRC_HIP_TYPE_Q5_0: return launch_type<TRC_HIP_TYPE_Q5_0>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream);
-        case TRC_HIP_TYPE_Q5_1: return launch_type<TRC_HIP_TYPE_Q5_1>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream);
-        case TRC_HIP_TYPE_Q8_0: return launch_type<TRC_HIP_TYPE_Q8_0>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream);
+        case TRC_HIP_TYPE_Q4_0: return launch_type<TRC_HIP_TYPE_Q4_0>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream, where);
+        case TRC_HIP_TYPE_Q4_1: return launch_type<TRC_HIP_TYPE_Q4_1>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream, where);
+        case TRC_HIP_TYPE_Q5_0: return launch_type<TRC_HIP_TYPE_Q5_0>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream, where);
+        case TRC_HIP_TYPE_Q5_1: return launch_type<TRC_HIP_TYPE_Q5_1>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream, where);
+        case TRC_HIP_TYPE_Q8_0: return launch_type<TRC_HIP_TYPE_Q8_0>(wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, stream, where);
         default: return fail(TRC_HIP_E_INVALID, "qmatvec: bad type %d", type);
     }
 }

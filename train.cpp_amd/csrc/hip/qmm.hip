@@ -768,14 +768,14 @@ bool qmm_supported(int64_t K, int64_t N, const void* wq, size_t nb1_w) {
 }
 
 int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, const float* x, int64_t N,
-               size_t nb1_x, float* y, size_t nb1_y, hipStream_t s) {
+               size_t nb1_x, float* y, size_t nb1_y, hipStream_t s, QmScratch where) {
     const int nblk = (int) (K / QK);
     if (nblk > QM_MAX_BLOCKS) {
         return fail(TRC_HIP_E_SHAPE, "qmm: K = %lld exceeds the %d the x workspace holds", (long long) K,
                     QM_MAX_BLOCKS * QK);
     }
     uint8_t* ws = nullptr;
-    const int rc = qm_stream_workspace(s, &ws);
+    const int rc = where == QmScratch::STATIC ? qm_static_scratch(&ws) : qm_stream_workspace(s, &ws);
     if (rc != TRC_HIP_OK) return rc;
     switch (type) {
         case TRC_HIP_TYPE_Q4_0: return launch_cols<TRC_HIP_TYPE_Q4_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
@@ -791,11 +791,25 @@ int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, con
 
 // ---------------------------------------------------------------- x workspaces
 //
-// One workspace per (device, stream), allocated by the first call on that
-// stream that takes this path and kept until the process ends. Work on one
-// stream runs in order, so calls on different streams never share x planes.
-// hipStreamPerThread names a different stream in every host thread, so its
-// workspaces are also keyed by thread.
+// trc_hip_qmatvec: one workspace per (device, stream), allocated by the first
+// call on that stream that takes this path and kept until the process ends.
+// Work on one stream runs in order, so calls on different streams never share
+// x planes. hipStreamPerThread names a different stream in every host thread,
+// so its workspaces are also keyed by thread.
+//
+// trc_hip_qmatvec_noalloc: the file-scope device array `scratch` below. Each GPU
+// holds its own copy at its own address, found once per device with
+// hipGetSymbolAddress; host code uses only that address, never the array's
+// name. Every call of that entry on one GPU shares the array, so such calls
+// that overlap on one GPU (other streams, concurrent graph replays) race.
+namespace trc_hip {
+namespace {
+constexpr size_t QM_WS_BYTES = (size_t) QM_A_BYTES + (size_t) QM_META_BYTES;
+}  // namespace
+}  // namespace trc_hip
+
+static __device__ __attribute__((aligned(256))) uint8_t scratch[trc_hip::QM_WS_BYTES];
+
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -803,8 +817,9 @@ int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, con
 namespace trc_hip {
 namespace {
 
-constexpr size_t QM_WS_BYTES = (size_t) QM_A_BYTES + (size_t) QM_META_BYTES;
+constexpr int QM_MAX_DEV = 64;
 std::mutex g_ws_mutex;
+uint8_t* g_scratch_dev[QM_MAX_DEV] = {};  // address of `scratch` on each device, once resolved
 
 struct StreamWs {
     int dev;
@@ -817,16 +832,48 @@ std::vector<StreamWs>& stream_workspaces() {
     return v;
 }
 
+int current_device(int* dev) {
+    const hipError_t e = hipGetDevice(dev);
+    if (e != hipSuccess) return hip_error(e, "hipGetDevice");
+    if (*dev < 0 || *dev >= QM_MAX_DEV) return fail(TRC_HIP_E_NO_DEVICE, "device %d out of range", *dev);
+    return TRC_HIP_OK;
+}
+
 }  // namespace
 
 size_t qm_workspace_bytes() {
     return QM_WS_BYTES;
 }
 
+int qm_scratch_setup() {
+    int dev = 0;
+    const int rc = current_device(&dev);
+    if (rc != TRC_HIP_OK) return rc;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    if (g_scratch_dev[dev] != nullptr) return TRC_HIP_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(TRC_HIP_E_INVALID, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_dev[dev] = (uint8_t*) p;
+    return TRC_HIP_OK;
+}
+
+int qm_static_scratch(uint8_t** ws) {
+    int rc = qm_scratch_setup();
+    if (rc != TRC_HIP_OK) return rc;
+    int dev = 0;
+    rc = current_device(&dev);
+    if (rc != TRC_HIP_OK) return rc;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    *ws = g_scratch_dev[dev];
+    return TRC_HIP_OK;
+}
+
 int qm_stream_workspace(hipStream_t s, uint8_t** ws) {
     int dev = 0;
-    const hipError_t ge = hipGetDevice(&dev);
-    if (ge != hipSuccess) return hip_error(ge, "hipGetDevice");
+    const int rc = current_device(&dev);
+    if (rc != TRC_HIP_OK) return rc;
     const std::thread::id tid = s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     for (const StreamWs& w : stream_workspaces()) {

@@ -23,7 +23,7 @@ EXPORTS = (
     "trc_hip_device_count", "trc_hip_init", "trc_hip_sync", "trc_hip_last_error",
     "trc_hip_malloc", "trc_hip_free", "trc_hip_h2d", "trc_hip_d2h", "trc_hip_memset",
     "trc_hip_fill_f32", "trc_hip_dequant", "trc_hip_mul_mat_f32", "trc_hip_qmatvec", "trc_hip_cpy",
-    "trc_hip_add_f32", "trc_hip_acc_f32", "trc_hip_repeat_back_f32",
+    "trc_hip_add_f32", "trc_hip_acc_f32", "trc_hip_repeat_back_f32", "trc_hip_qmatvec_noalloc",
 )
 
 
@@ -92,6 +92,7 @@ def load() -> C.CDLL:
         "trc_hip_dequant": ([I, P, I64, P, P], I),
         "trc_hip_mul_mat_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_qmatvec": ([I, P, I64, I64, SZ, P, I64, SZ, P, SZ, P], I),
+        "trc_hip_qmatvec_noalloc": ([I, P, I64, I64, SZ, P, I64, SZ, P, SZ, P], I),
         "trc_hip_cpy": ([C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_add_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_acc_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), SZ, SZ, SZ, SZ, I, P], I),
@@ -143,6 +144,11 @@ def mul_mat_f32(a: Tensor, b: Tensor, d: Tensor, stream: int | None = None) -> N
 def qmatvec(type_: int, w_ptr: int, K: int, M: int, nb1_w: int, x_ptr: int, N: int, nb1_x: int,
             y_ptr: int, nb1_y: int, stream: int | None = None) -> None:
     check(load().trc_hip_qmatvec(type_, w_ptr, K, M, nb1_w, x_ptr, N, nb1_x, y_ptr, nb1_y, stream))
+
+
+def qmatvec_noalloc(type_: int, w_ptr: int, K: int, M: int, nb1_w: int, x_ptr: int, N: int, nb1_x: int,
+                    y_ptr: int, nb1_y: int, stream: int | None = None) -> None:
+    check(load().trc_hip_qmatvec_noalloc(type_, w_ptr, K, M, nb1_w, x_ptr, N, nb1_x, y_ptr, nb1_y, stream))
 
 
 def cpy(src: Tensor, dst: Tensor, stream: int | None = None) -> None:
