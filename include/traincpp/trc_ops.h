@@ -1,7 +1,8 @@
 // traincpp-compatible operator constructors used on the HIP backend's path
 // (subset of include/traincpp/trc_ops.h in the reference: views, cont, cast,
-// dup, mul_mat, and the add / acc / repeat_back nodes mul_mat's autograd
-// emits). They only build graph nodes; no computation happens here.
+// dup, mul_mat, and the add / mul / sum / repeat / acc / repeat_back nodes of a
+// Linear layer's loss and autograd). They only build graph nodes; no
+// computation happens here.
 #pragma once
 
 #include "trc_context.h"
@@ -35,6 +36,15 @@ Tensor* mul_mat(Context* ctx, Tensor* a, Tensor* b);
 
 // a + b with b broadcast to a's shape (each b dim equal to a's or 1); result has a's shape.
 Tensor* add(Context* ctx, Tensor* a, Tensor* b);
+
+// a * b with b broadcast to a's shape; result has a's shape.
+Tensor* mul(Context* ctx, Tensor* a, Tensor* b);
+
+// Sum of every element of a, as a one-element tensor of a's type.
+Tensor* sum(Context* ctx, Tensor* a);
+
+// a broadcast to target's shape (each a dim equal to target's or 1).
+Tensor* repeat(Context* ctx, Tensor* a, Tensor* target);
 
 // Sum of a over its repeats back to b's shape (a.ne[i] % b.ne[i] == 0).
 Tensor* repeat_back(Context* ctx, Tensor* a, Tensor* b);

@@ -197,6 +197,27 @@ int trc_hip_cpy(const trc_hip_tensor* src, const trc_hip_tensor* dst, void* stre
  * result is bit-identical to the CPU's. F32 only. */
 int trc_hip_add_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst, void* stream);
 
+/* ggml mul, dst = a * b, with the broadcast and layouts of trc_hip_add_f32.
+ * OP_MUL (src/ops/trc_ops.cpp:59-61) as computed by compute_binary with fn_mul
+ * (src/backends/cpu/trc_cpu_ops.cpp:49, 52-78): one rounding per element, so the
+ * result is bit-identical to the CPU's. F32 only. */
+int trc_hip_mul_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst, void* stream);
+
+/* ggml repeat: dst[i0..i3] = a[i0 % a.ne0, .., i3 % a.ne3] for any strides; every
+ * dst->ne[d] a multiple of a->ne[d]. OP_REPEAT (src/ops/trc_ops.cpp:447-456) as
+ * computed by compute_repeat (src/backends/cpu/trc_cpu_ops.cpp:913-928): an F32
+ * copy, bit-identical. */
+int trc_hip_repeat_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream);
+
+/* ggml sum: the one element of dst = the sum of every element of a (any strides).
+ * OP_SUM (src/ops/trc_ops.cpp:214-221) as computed by compute_sum
+ * (src/backends/cpu/trc_cpu_ops.cpp:302-315, row_sum_f32 :284-300): each row
+ * (ne0-run) is summed in double from 0 in element order, the row sums are added
+ * in double in row order, and the total is rounded to float once; the same
+ * operations in the same order, so the result is bit-identical. One workgroup:
+ * meant for losses, not bulk reductions. */
+int trc_hip_sum_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream);
+
 /* ggml acc: dst = a, then dst[offset + i0*4 + i1*nb1 + i2*nb2 + i3*nb3] += b[i]
  * for every element of b. OP_ACC (src/core/trc_tensor.cpp:322-361, computed by
  * compute_acc src/backends/cpu/trc_cpu_ops.cpp:954-999). a and dst contiguous

@@ -291,9 +291,15 @@ static size_t bcast_offset(const int64_t t_ne[4], const size_t t_nb[4], const in
 
 static int64_t nelem(const int64_t ne[4]) { return ne[0] * ne[1] * ne[2] * ne[3]; }
 
-int orc_add(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
-            const void* b, const int64_t b_ne[4], const size_t b_nb[4],
-            void* d, const int64_t d_ne[4], const size_t d_nb[4]) {
+// compute_binary's general path (src/backends/cpu/trc_cpu_ops.cpp:52-78): a and
+// dst walked in linear order, b through the broadcast offset; one float
+// operation per element (fn_add / fn_mul, :47-49).
+}  // extern "C"
+
+template <typename Fn>
+static int binary_f32(const void* a, const int64_t a_ne[4], const size_t a_nb[4], const void* b,
+                      const int64_t b_ne[4], const size_t b_nb[4], void* d, const int64_t d_ne[4],
+                      const size_t d_nb[4], Fn fn) {
     for (int k = 0; k < 4; ++k) {
         if (d_ne[k] != a_ne[k] || (b_ne[k] != a_ne[k] && b_ne[k] != 1)) return -1;
     }
@@ -304,7 +310,64 @@ int orc_add(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
     for (int64_t i = 0; i < n; ++i) {
         const float va = *(const float*) (pa + lin_offset(a_ne, a_nb, i));
         const float vb = *(const float*) (pb + bcast_offset(b_ne, b_nb, d_ne, i));
-        *(float*) (pd + lin_offset(d_ne, d_nb, i)) = va + vb;
+        *(float*) (pd + lin_offset(d_ne, d_nb, i)) = fn(va, vb);
+    }
+    return 0;
+}
+
+extern "C" {
+
+int orc_add(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
+            const void* b, const int64_t b_ne[4], const size_t b_nb[4],
+            void* d, const int64_t d_ne[4], const size_t d_nb[4]) {
+    return binary_f32(a, a_ne, a_nb, b, b_ne, b_nb, d, d_ne, d_nb, [](float x, float y) { return x + y; });
+}
+
+int orc_mul(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
+            const void* b, const int64_t b_ne[4], const size_t b_nb[4],
+            void* d, const int64_t d_ne[4], const size_t d_nb[4]) {
+    return binary_f32(a, a_ne, a_nb, b, b_ne, b_nb, d, d_ne, d_nb, [](float x, float y) { return x * y; });
+}
+
+// compute_sum (src/backends/cpu/trc_cpu_ops.cpp:302-315): rows in the order i3,
+// i2, i1; each row summed in double from 0 along i0 (row_sum_f32 :284-300); the
+// row sums added in double; one rounding to float.
+int orc_sum(const void* a, const int64_t a_ne[4], const size_t a_nb[4], float* out) {
+    const uint8_t* pa = (const uint8_t*) a;
+    double sum = 0.0;
+    for (int64_t i3 = 0; i3 < a_ne[3]; ++i3) {
+        for (int64_t i2 = 0; i2 < a_ne[2]; ++i2) {
+            for (int64_t i1 = 0; i1 < a_ne[1]; ++i1) {
+                const uint8_t* row = pa + (size_t) i1 * a_nb[1] + (size_t) i2 * a_nb[2] + (size_t) i3 * a_nb[3];
+                double rs = 0.0;
+                for (int64_t i0 = 0; i0 < a_ne[0]; ++i0) rs += *(const float*) (row + (size_t) i0 * a_nb[0]);
+                sum += rs;
+            }
+        }
+    }
+    *out = (float) sum;
+    return 0;
+}
+
+// compute_repeat (src/backends/cpu/trc_cpu_ops.cpp:913-928): dst element i (linear
+// order over d_ne) takes a's element at index (i_k % a_ne[k]), extent-1 dims at 0.
+int orc_repeat(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const int64_t d_ne[4],
+               const size_t d_nb[4]) {
+    for (int k = 0; k < 4; ++k) {
+        if (a_ne[k] <= 0 || d_ne[k] % a_ne[k] != 0) return -1;
+    }
+    const uint8_t* pa = (const uint8_t*) a;
+    uint8_t* pd = (uint8_t*) d;
+    const int64_t n = nelem(d_ne);
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t rem = i;
+        size_t oa = 0;
+        for (int k = 0; k < 4; ++k) {
+            const int64_t idx = rem % d_ne[k];
+            rem /= d_ne[k];
+            oa += (size_t) (a_ne[k] == 1 ? 0 : idx % a_ne[k]) * a_nb[k];
+        }
+        *(float*) (pd + lin_offset(d_ne, d_nb, i)) = *(const float*) (pa + oa);
     }
     return 0;
 }

@@ -36,6 +36,18 @@
  *   orc_repeat_back    - tests/test_ops.cpp:1128-1150, numpy's reshape-and-sum
  *                        (float64 bound), and the reference's compute_repeat_back
  *                        (oracle/_ref), bit for bit.
+ *   orc_mul            - the product step of tests/test_ops.cpp:98-118, the PyTorch
+ *                        golden tests/golden/mul_same_*, numpy's float32 a * b with
+ *                        broadcasting, and the reference's compute_binary
+ *                        (oracle/_ref), bit for bit.
+ *   orc_sum            - the PyTorch golden tests/golden/sum_*, order-revealing
+ *                        cases whose double sums differ by summation order (within
+ *                        a row, across rows and planes) or by accumulating in float,
+ *                        math.fsum within one float rounding on random data, and
+ *                        the reference's compute_sum (oracle/_ref), bit for bit.
+ *   orc_repeat         - tests/test_ops.cpp:795-815, the PyTorch golden
+ *                        tests/golden/repeat_*, numpy's tile, and the reference's
+ *                        compute_repeat (oracle/_ref), bit for bit.
  */
 #pragma once
 
@@ -106,6 +118,21 @@ int orc_acc(const void* a, const int64_t a_ne[4], const void* b, const int64_t b
  * (src/ops/trc_ops.cpp:458-470, compute_repeat_back
  * src/backends/cpu/trc_cpu_ops.cpp:932-952). Returns 0, or -1 on bad shapes. */
 int orc_repeat_back(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const int64_t d_ne[4]);
+
+/* mul: d = a * b with a's shape, b broadcast (src/ops/trc_ops.cpp:59-61,
+ * compute_binary src/backends/cpu/trc_cpu_ops.cpp:52-78). */
+int orc_mul(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
+            const void* b, const int64_t b_ne[4], const size_t b_nb[4],
+            void* d, const int64_t d_ne[4], const size_t d_nb[4]);
+
+/* sum of all elements of a strided F32 tensor (src/ops/trc_ops.cpp:214-221,
+ * compute_sum src/backends/cpu/trc_cpu_ops.cpp:302-315). */
+int orc_sum(const void* a, const int64_t a_ne[4], const size_t a_nb[4], float* out);
+
+/* repeat of a to d's shape (src/ops/trc_ops.cpp:447-456, compute_repeat
+ * src/backends/cpu/trc_cpu_ops.cpp:913-928). */
+int orc_repeat(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const int64_t d_ne[4],
+               const size_t d_nb[4]);
 
 /* splitmix64 stream (src/core/trc_rng.cpp:38-68). */
 uint64_t orc_rng_next_u64(uint64_t* state);

@@ -14,6 +14,8 @@
 //                    src/backends/cpu/trc_cpu_ops.cpp:954)
 //   ref_repeat_back -> permute view + repeat_back + CPU Device
 //                    (src/ops/trc_ops.cpp:458, src/backends/cpu/trc_cpu_ops.cpp:932)
+//   ref_mul / ref_sum / ref_repeat -> permute views + mul / sum / repeat + CPU
+//                    Device (src/ops/trc_ops.cpp:59,214,447; trc_cpu_ops.cpp:52,302,913)
 //   ref_fp16_*    -> core/trc_float.h:23-63
 //   ref_rng_*     -> src/core/trc_rng.cpp:38-68
 #include "traincpp/traincpp.h"
@@ -186,6 +188,67 @@ int ref_repeat_back(const float* a, const int64_t a_ne[4], const int pa[4], cons
     Tensor* ta = new_tensor_4d(ctx, TYPE_F32, a_ne[0], a_ne[1], a_ne[2], a_ne[3]);
     Tensor* shape = new_tensor_4d(ctx, TYPE_F32, d_ne[0], d_ne[1], d_ne[2], d_ne[3]);
     Tensor* r = repeat_back(ctx, permute(ctx, ta, pa[0], pa[1], pa[2], pa[3]), shape);
+    Graph* g = graph_new(ctx);
+    graph_build_forward_expand(ctx, g, r);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    tensor_set(ta, a, 0, tensor_nbytes(ta));
+    const bool ok = dev->graph_compute(g);
+    tensor_get(r, out, 0, tensor_nbytes(r));
+    buffer_free(buf);
+    graph_free(g);
+    context_free(ctx);
+    return ok ? 0 : -2;
+}
+
+// mul(permute(a), permute(b)); out gets a's (viewed) shape, contiguous.
+int ref_mul(const float* a, const int64_t a_ne[4], const int pa[4], const float* b, const int64_t b_ne[4],
+            const int pb[4], float* out) {
+    Device* dev = device_cpu();
+    if (!dev) return -1;
+    Context* ctx = context_new(1 << 20);
+    Tensor* ta = new_tensor_4d(ctx, TYPE_F32, a_ne[0], a_ne[1], a_ne[2], a_ne[3]);
+    Tensor* tb = new_tensor_4d(ctx, TYPE_F32, b_ne[0], b_ne[1], b_ne[2], b_ne[3]);
+    Tensor* r = mul(ctx, permute(ctx, ta, pa[0], pa[1], pa[2], pa[3]), permute(ctx, tb, pb[0], pb[1], pb[2], pb[3]));
+    Graph* g = graph_new(ctx);
+    graph_build_forward_expand(ctx, g, r);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    tensor_set(ta, a, 0, tensor_nbytes(ta));
+    tensor_set(tb, b, 0, tensor_nbytes(tb));
+    const bool ok = dev->graph_compute(g);
+    tensor_get(r, out, 0, tensor_nbytes(r));
+    buffer_free(buf);
+    graph_free(g);
+    context_free(ctx);
+    return ok ? 0 : -2;
+}
+
+// sum(permute(a)) into *out.
+int ref_sum(const float* a, const int64_t a_ne[4], const int pa[4], float* out) {
+    Device* dev = device_cpu();
+    if (!dev) return -1;
+    Context* ctx = context_new(1 << 20);
+    Tensor* ta = new_tensor_4d(ctx, TYPE_F32, a_ne[0], a_ne[1], a_ne[2], a_ne[3]);
+    Tensor* r = sum(ctx, permute(ctx, ta, pa[0], pa[1], pa[2], pa[3]));
+    Graph* g = graph_new(ctx);
+    graph_build_forward_expand(ctx, g, r);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    tensor_set(ta, a, 0, tensor_nbytes(ta));
+    const bool ok = dev->graph_compute(g);
+    tensor_get(r, out, 0, sizeof(float));
+    buffer_free(buf);
+    graph_free(g);
+    context_free(ctx);
+    return ok ? 0 : -2;
+}
+
+// repeat(permute(a), target of shape d_ne); out contiguous with d_ne.
+int ref_repeat(const float* a, const int64_t a_ne[4], const int pa[4], const int64_t d_ne[4], float* out) {
+    Device* dev = device_cpu();
+    if (!dev) return -1;
+    Context* ctx = context_new(1 << 20);
+    Tensor* ta = new_tensor_4d(ctx, TYPE_F32, a_ne[0], a_ne[1], a_ne[2], a_ne[3]);
+    Tensor* target = new_tensor_4d(ctx, TYPE_F32, d_ne[0], d_ne[1], d_ne[2], d_ne[3]);
+    Tensor* r = repeat(ctx, permute(ctx, ta, pa[0], pa[1], pa[2], pa[3]), target);
     Graph* g = graph_new(ctx);
     graph_build_forward_expand(ctx, g, r);
     Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());

@@ -50,6 +50,12 @@ def oracle() -> C.CDLL:
         lib.orc_acc.restype = I
         lib.orc_repeat_back.argtypes = [P, NE, NB, P, NE]
         lib.orc_repeat_back.restype = I
+        lib.orc_mul.argtypes = [P, NE, NB, P, NE, NB, P, NE, NB]
+        lib.orc_mul.restype = I
+        lib.orc_sum.argtypes = [P, NE, NB, C.POINTER(F)]
+        lib.orc_sum.restype = I
+        lib.orc_repeat.argtypes = [P, NE, NB, P, NE, NB]
+        lib.orc_repeat.restype = I
         lib.orc_rng_next_u64.argtypes = [C.POINTER(C.c_uint64)]
         lib.orc_rng_next_u64.restype = C.c_uint64
         lib.orc_rng_uniform01.argtypes = [C.POINTER(C.c_uint64)]
@@ -82,6 +88,12 @@ def ref() -> C.CDLL:
         lib.ref_acc.restype = I
         lib.ref_repeat_back.argtypes = [P, NE, AX, NE, P]
         lib.ref_repeat_back.restype = I
+        lib.ref_mul.argtypes = [P, NE, AX, P, NE, AX, P]
+        lib.ref_mul.restype = I
+        lib.ref_sum.argtypes = [P, NE, AX, C.POINTER(F)]
+        lib.ref_sum.restype = I
+        lib.ref_repeat.argtypes = [P, NE, AX, NE, P]
+        lib.ref_repeat.restype = I
         for n in ("ref_rng_next_u64", "ref_rng_uniform01"):
             getattr(lib, n).argtypes = [C.POINTER(C.c_uint64)]
         lib.ref_rng_next_u64.restype = C.c_uint64
@@ -195,6 +207,37 @@ def acc(a: np.ndarray, b: np.ndarray, nb1: int, nb2: int, nb3: int, offset: int,
     return out
 
 
+def mul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Oracle mul of two (possibly strided) float32 views; result contiguous with a's shape."""
+    pa, ane, anb = base_ptr_and_meta(a)
+    pb, bne, bnb = base_ptr_and_meta(b)
+    out = np.zeros(ggml_shape(ane), dtype=np.float32)
+    _, dne, dnb = base_ptr_and_meta(out)
+    rc = oracle().orc_mul(pa, NE(*ane), NB(*anb), pb, NE(*bne), NB(*bnb), out.ctypes.data, NE(*dne), NB(*dnb))
+    assert rc == 0, rc
+    return out
+
+
+def sum_all(a: np.ndarray) -> np.float32:
+    """Oracle sum of every element of a (possibly strided) float32 view."""
+    pa, ane, anb = base_ptr_and_meta(a)
+    out = F(0.0)
+    rc = oracle().orc_sum(pa, NE(*ane), NB(*anb), C.byref(out))
+    assert rc == 0, rc
+    return np.float32(out.value)
+
+
+def repeat(a: np.ndarray, d_ne) -> np.ndarray:
+    """Oracle repeat of a (possibly strided) view to ggml shape d_ne; contiguous result."""
+    pa, ane, anb = base_ptr_and_meta(a)
+    d_ne = list(d_ne) + [1] * (4 - len(d_ne))
+    out = np.zeros(ggml_shape(d_ne), dtype=np.float32)
+    _, _, dnb = base_ptr_and_meta(out)
+    rc = oracle().orc_repeat(pa, NE(*ane), NB(*anb), out.ctypes.data, NE(*d_ne), NB(*dnb))
+    assert rc == 0, rc
+    return out
+
+
 def repeat_back(a: np.ndarray, d_ne) -> np.ndarray:
     """Oracle repeat_back of a (possibly strided) view onto ggml shape d_ne; contiguous result."""
     pa, ane, anb = base_ptr_and_meta(a)
@@ -250,3 +293,36 @@ def row_l2_error(got: np.ndarray, want: np.ndarray) -> float:
     w = want.reshape(-1, want.shape[-1]).astype(np.float64)
     norms = np.maximum(np.sqrt((w * w).sum(axis=1)), 1e-30)
     return float((np.abs(g - w).max(axis=1) / norms).max())
+
+
+def ref_mul(a_base: np.ndarray, pa, b_base: np.ndarray, pb) -> np.ndarray:
+    """Reference library mul(permute(A, pa), permute(B, pb)) on its CPU device."""
+    a_base = np.ascontiguousarray(a_base, dtype=np.float32)
+    b_base = np.ascontiguousarray(b_base, dtype=np.float32)
+    ane = list(a_base.shape)[::-1] + [1] * (4 - a_base.ndim)
+    bne = list(b_base.shape)[::-1] + [1] * (4 - b_base.ndim)
+    out = np.zeros(ggml_shape(_perm_ne(ane, pa)), dtype=np.float32)
+    rc = ref().ref_mul(a_base.ctypes.data, NE(*ane), AX(*pa), b_base.ctypes.data, NE(*bne), AX(*pb), out.ctypes.data)
+    assert rc == 0, rc
+    return out
+
+
+def ref_sum(a_base: np.ndarray, pa) -> np.float32:
+    """Reference library sum(permute(A, pa)) on its CPU device."""
+    a_base = np.ascontiguousarray(a_base, dtype=np.float32)
+    ane = list(a_base.shape)[::-1] + [1] * (4 - a_base.ndim)
+    out = F(0.0)
+    rc = ref().ref_sum(a_base.ctypes.data, NE(*ane), AX(*pa), C.byref(out))
+    assert rc == 0, rc
+    return np.float32(out.value)
+
+
+def ref_repeat(a_base: np.ndarray, pa, d_ne) -> np.ndarray:
+    """Reference library repeat(permute(A, pa), target of shape d_ne) on its CPU device."""
+    a_base = np.ascontiguousarray(a_base, dtype=np.float32)
+    ane = list(a_base.shape)[::-1] + [1] * (4 - a_base.ndim)
+    d_ne = list(d_ne) + [1] * (4 - len(d_ne))
+    out = np.zeros(ggml_shape(d_ne), dtype=np.float32)
+    rc = ref().ref_repeat(a_base.ctypes.data, NE(*ane), AX(*pa), NE(*d_ne), out.ctypes.data)
+    assert rc == 0, rc
+    return out

@@ -152,3 +152,99 @@ def test_repeat_back_mul_mat_broadcast_shape(hip):
     da.free()
     out.free()
     assert (bits(got) == bits(O.repeat_back(A, [128, 1024, 8, 4]))).all()
+
+
+# ---------------------------------------------------------------- mul / repeat / sum
+# trc_hip_mul_f32 / trc_hip_repeat_f32 / trc_hip_sum_f32 against orc_mul /
+# orc_repeat / orc_sum (compute_binary, compute_repeat, compute_sum): bitwise.
+
+def gpu_mul(a_base, a_view, b_base, b_view):
+    da, db = Dev(a_base), Dev(b_base)
+    ne, _ = O.view_meta(a_view)
+    out = empty(O.ggml_shape(ne))
+    H.mul_f32(da.tensor(a_view), db.tensor(b_view), out.tensor())
+    H.sync()
+    r = out.read()
+    for d in (da, db, out):
+        d.free()
+    return r
+
+
+@pytest.mark.parametrize("bshape", [(3, 5, 7, 33), (1, 5, 7, 33), (3, 1, 7, 1), (1, 1, 1, 33), (1, 1, 1, 1)])
+def test_mul_broadcast_bitwise(hip, bshape):
+    announce(f"mul bcast {bshape}")
+    rng = np.random.default_rng(21)
+    a = rng.standard_normal((3, 5, 7, 33)).astype(np.float32)
+    b = rng.standard_normal(bshape).astype(np.float32)
+    assert (bits(gpu_mul(a, a, b, b)) == bits(O.mul(a, b))).all()
+
+
+def test_mul_strided_and_linear_loss_shape(hip):
+    """The loss product of a Linear layer: y [4096, 512] times a constant of the
+    same shape, and a transposed operand."""
+    rng = np.random.default_rng(22)
+    y = rng.standard_normal((512, 4096)).astype(np.float32)
+    g = (rng.standard_normal((512, 4096)) * 1e-2).astype(np.float32)
+    assert (bits(gpu_mul(y, y, g, g)) == bits(O.mul(y, g))).all()
+    A = rng.standard_normal((40, 30)).astype(np.float32)
+    B = rng.standard_normal((30, 40)).astype(np.float32)
+    assert (bits(gpu_mul(A, A.T, B, B)) == bits(O.mul(A.T, B))).all()
+
+
+def gpu_repeat(a_base, a_view, d_ne):
+    da = Dev(a_base)
+    out = empty(O.ggml_shape(d_ne))
+    H.repeat_f32(da.tensor(a_view), out.tensor())
+    H.sync()
+    r = out.read()
+    da.free()
+    out.free()
+    return r
+
+
+@pytest.mark.parametrize("ashape,d_ne", [((1, 1, 1, 1), [4096, 512, 1, 1]), ((1, 1, 1, 7), [7, 33, 5, 3]),
+                                         ((3, 1, 5, 1), [9, 5, 1, 3]), ((1, 1, 1, 1), [1, 1, 1, 1])])
+def test_repeat_bitwise(hip, ashape, d_ne):
+    announce(f"repeat {ashape} -> {d_ne}")
+    rng = np.random.default_rng(23)
+    a = rng.standard_normal(ashape).astype(np.float32)
+    assert (bits(gpu_repeat(a, a, d_ne)) == bits(O.repeat(a, d_ne))).all()
+
+
+def test_repeat_strided_source_bitwise(hip):
+    rng = np.random.default_rng(24)
+    A = rng.standard_normal((6, 1, 9)).astype(np.float32)
+    av = A.transpose(1, 2, 0)  # ggml [6, 9, 1] with nb0 = 36 B
+    assert (bits(gpu_repeat(A, av, [6, 9, 4, 2])) == bits(O.repeat(av, [6, 9, 4, 2]))).all()
+
+
+def gpu_sum(a_base, a_view):
+    da = Dev(a_base)
+    out = empty((1,))
+    H.sum_f32(da.tensor(a_view), out.tensor())
+    H.sync()
+    r = out.read()[0]
+    da.free()
+    out.free()
+    return np.float32(r)
+
+
+@pytest.mark.parametrize("shape", [(512, 4096), (3, 5, 7, 33), (1, 1, 1, 1), (2, 3, 1500, 5), (1, 1, 2500, 3)])
+def test_sum_bitwise(hip, shape):
+    """Rows of every length, more rows than the 1024 the kernel sums per pass,
+    and the Linear loss shape [4096, 512]."""
+    announce(f"sum {shape}")
+    rng = np.random.default_rng(25)
+    a = (rng.standard_normal(shape) * 10.0 ** rng.integers(-3, 4, shape)).astype(np.float32)
+    assert bits(gpu_sum(a, a)) == bits(O.sum_all(a))
+
+
+def test_sum_order_and_strides_bitwise(hip):
+    big = np.float32(2.0 ** 53)
+    for arr in (np.array([big, 1, -big], np.float32), np.array([big, 1, -big], np.float32).reshape(3, 1),
+                np.array([-big, 1, big], np.float32).reshape(3, 1, 1)):
+        assert bits(gpu_sum(arr, arr)) == bits(O.sum_all(arr))
+    rng = np.random.default_rng(26)
+    A = rng.standard_normal((6, 70, 50)).astype(np.float32)
+    av = A.transpose(2, 0, 1)  # strided rows
+    assert bits(gpu_sum(A, av)) == bits(O.sum_all(av))

@@ -177,3 +177,134 @@ def test_repeat_back_bitwise_vs_reference(pa, d_ne):
     av = np.transpose(A, [3 - pa[3 - k] for k in range(4)])
     got = O.repeat_back(av, d_ne)
     assert (_bits(got) == _bits(want)).all()
+
+
+# ---------------------------------------------------------------- mul / sum / repeat
+# The nodes of a Linear layer's scalar loss (sum(mul(y, g))) and its backward
+# (repeat of the loss gradient): tests/test_ops.cpp:98-118, 795-815 and the
+# PyTorch goldens mul_same_*, sum_*, repeat_* (tests/golden/cases.txt:3,30,41).
+
+def test_mul_kat():
+    # the product step of tests/test_ops.cpp:98-118: (a - b) * a
+    a = np.array([4, 6, 8], np.float32)
+    b = np.array([2, 3, 4], np.float32)
+    assert (O.mul(a - b, a) == [8, 18, 32]).all()
+
+
+def test_mul_golden():
+    a = np.load(GOLDEN / "mul_same_in0.npy", allow_pickle=False).astype(np.float32)
+    b = np.load(GOLDEN / "mul_same_in1.npy", allow_pickle=False).astype(np.float32)
+    want = np.load(GOLDEN / "mul_same_out.npy", allow_pickle=False)
+    assert np.allclose(O.mul(a, b), want, atol=1e-4, rtol=1e-3)
+
+
+def test_mul_matches_numpy_broadcast_bitwise():
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((3, 5, 7, 9)).astype(np.float32)
+    for bshape in [(3, 5, 7, 9), (1, 5, 7, 9), (3, 1, 7, 1), (1, 1, 1, 9), (1, 1, 1, 1)]:
+        b = rng.standard_normal(bshape).astype(np.float32)
+        assert (_bits(O.mul(a, b)) == _bits(a * b)).all(), bshape
+    at = a.transpose(0, 2, 1, 3)
+    b = rng.standard_normal((1, 7, 1, 9)).astype(np.float32)
+    assert (_bits(O.mul(at, b)) == _bits(at * b)).all()
+
+
+def test_repeat_kat_and_golden():
+    # tests/test_ops.cpp:795-815: [1, 2] repeated to ggml [2, 3]
+    assert (O.repeat(np.array([1, 2], np.float32), [2, 3]).reshape(-1) == [1, 2, 1, 2, 1, 2]).all()
+    a = np.load(GOLDEN / "repeat_in0.npy", allow_pickle=False).astype(np.float32)
+    want = np.load(GOLDEN / "repeat_out.npy", allow_pickle=False)
+    got = O.repeat(a, [2, 3, 1, 1])  # tests/golden/cases.txt:41 target ne = [2, 3, 1, 1]
+    assert np.allclose(got, want.reshape(got.shape), atol=1e-4, rtol=1e-3)
+
+
+def test_repeat_matches_numpy_tile():
+    rng = np.random.default_rng(12)
+    for ashape, reps in [((1, 1, 1, 1), (2, 3, 4, 5)), ((1, 3, 1, 5), (2, 1, 4, 1)), ((2, 3, 4, 5), (1, 2, 1, 3))]:
+        a = rng.standard_normal(ashape).astype(np.float32)
+        want = np.tile(a, reps)
+        assert (_bits(O.repeat(a, list(want.shape)[::-1])) == _bits(want)).all()
+    a = rng.standard_normal((3, 4)).astype(np.float32).T  # strided source
+    assert (_bits(O.repeat(a, [3, 8])) == _bits(np.tile(a, (2, 1)))).all()
+
+
+def test_sum_golden():
+    a = np.load(GOLDEN / "sum_in0.npy", allow_pickle=False).astype(np.float32)
+    want = np.load(GOLDEN / "sum_out.npy", allow_pickle=False).reshape(())
+    assert np.isclose(O.sum_all(a), want, atol=1e-4, rtol=1e-3)
+
+
+def test_sum_order_is_revealed():
+    big = np.float32(2.0 ** 53)
+    # within a row, in double: (2^53 + 1) rounds back to 2^53, so the row is 0
+    # (exactly 1 in any other order)
+    assert O.sum_all(np.array([big, 1, -big], np.float32)) == 0
+    assert O.sum_all(np.array([big, -big, 1], np.float32)) == 1
+    # across rows (i1 fastest) and planes (i2, then i3): the same cancellation
+    assert O.sum_all(np.array([big, 1, -big], np.float32).reshape(3, 1)) == 0
+    assert O.sum_all(np.array([big, 1, -big], np.float32).reshape(3, 1, 1)) == 0
+    assert O.sum_all(np.array([big, 1, -big], np.float32).reshape(3, 1, 1, 1)) == 0
+    assert O.sum_all(np.array([-big, 1, big], np.float32).reshape(3, 1)) == 1
+    # double, not float, accumulation: 2^24 + 16 ones stays exact
+    row = np.concatenate([[np.float32(2.0 ** 24)], np.ones(16, np.float32)]).astype(np.float32)
+    assert O.sum_all(row) == np.float32(2.0 ** 24 + 16)
+
+
+def test_sum_within_one_rounding_of_exact():
+    import math
+    rng = np.random.default_rng(13)
+    a = (rng.standard_normal((3, 4, 50, 70)) * 10.0 ** rng.integers(-3, 4, (3, 4, 50, 70))).astype(np.float32)
+    exact = math.fsum(a.astype(np.float64).reshape(-1))
+    got = float(O.sum_all(a))
+    # double partial sums carry ~1e-16 relative error per add over 42000 terms,
+    # then one float rounding: within 2 float ulps of the exact sum
+    assert abs(got - exact) <= 2 * np.spacing(np.float32(abs(exact))) + 1e-9 * np.abs(a).sum()
+
+
+@pytestmark_ref
+@pytest.mark.parametrize("pa,pb,bshape", [((0, 1, 2, 3), (0, 1, 2, 3), None), ((1, 0, 2, 3), (0, 1, 2, 3), (2,))])
+def test_mul_bitwise_vs_reference(pa, pb, bshape):
+    rng = np.random.default_rng(14)
+    A = rng.standard_normal((3, 4, 5, 6)).astype(np.float32)
+    ane = [6, 5, 4, 3]
+    ape = [ane[pa[i]] for i in range(4)]
+    bne = list(ape)
+    if bshape is not None:
+        for k in bshape:
+            bne[k] = 1
+    inv = [0] * 4
+    for i in range(4):
+        inv[pb[i]] = i
+    b_base_ne = [bne[inv[k]] for k in range(4)]
+    B = rng.standard_normal(tuple(b_base_ne[::-1])).astype(np.float32)
+    want = O.ref_mul(A, pa, B, pb)
+    av = np.transpose(A, [3 - pa[3 - k] for k in range(4)])
+    bv = np.transpose(B, [3 - pb[3 - k] for k in range(4)])
+    assert (_bits(O.mul(av, bv)) == _bits(want)).all()
+
+
+@pytestmark_ref
+@pytest.mark.parametrize("pa", [(0, 1, 2, 3), (1, 0, 2, 3), (0, 2, 1, 3), (2, 3, 0, 1)])
+def test_sum_bitwise_vs_reference(pa):
+    rng = np.random.default_rng(15)
+    A = (rng.standard_normal((4, 6, 5, 300)) * 1e3).astype(np.float32)  # base ggml [300, 5, 6, 4]
+    want = O.ref_sum(A, pa)
+    av = np.transpose(A, [3 - pa[3 - k] for k in range(4)])
+    assert _bits(O.sum_all(av)) == _bits(want)
+
+
+@pytestmark_ref
+@pytest.mark.parametrize("ashape,pa,d_ne", [
+    # the reference's repeat broadcasts extent-1 dims only (tensor_can_repeat,
+    # src/core/trc_tensor.cpp:81-88)
+    ((4, 6, 1, 8), (0, 1, 2, 3), [8, 10, 6, 4]),
+    ((4, 6, 1, 8), (1, 0, 2, 3), [10, 8, 6, 4]),
+    ((1, 6, 5, 1), (0, 2, 1, 3), [7, 6, 5, 3]),
+    ((1, 1, 1, 1), (0, 1, 2, 3), [9, 4, 3, 2]),
+])
+def test_repeat_bitwise_vs_reference(ashape, pa, d_ne):
+    rng = np.random.default_rng(16)
+    A = rng.standard_normal(ashape).astype(np.float32)
+    want = O.ref_repeat(A, pa, d_ne)
+    av = np.transpose(A, [3 - pa[3 - k] for k in range(4)])
+    assert (_bits(O.repeat(av, d_ne)) == _bits(want)).all()

@@ -208,7 +208,17 @@ public:
                        t->nb[0] == sizeof(float);
             }
             case OP_ADD:  // compute_binary: b broadcasts where its extent is 1
+            case OP_MUL:
                 return is_f32(a) && is_f32(b) && is_f32(t) && tensor_are_same_shape(a, t) && tensor_can_repeat(b, a);
+            case OP_SUM:
+                return is_f32(a) && is_f32(t) && tensor_nelements(t) == 1;
+            case OP_REPEAT: {
+                if (!is_f32(a) || !is_f32(t)) return false;
+                for (int i = 0; i < 4; ++i) {
+                    if (t->ne[i] % a->ne[i] != 0) return false;
+                }
+                return true;
+            }
             case OP_ACC: {
                 if (!is_f32(a) || !is_f32(b) || !is_f32(t) || !tensor_are_same_shape(a, t)) return false;
                 if (!tensor_is_contiguous(a) || !tensor_is_contiguous(t)) return false;
@@ -315,11 +325,28 @@ private:
                     mul_mat_quant(t);
                 }
                 return;
-            case OP_ADD: {
+            case OP_ADD:
+            case OP_MUL: {
                 const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
                 const trc_hip_tensor b = describe(t->src[1], need_buffer(t->src[1]));
                 const trc_hip_tensor d = describe(t, need_buffer(t));
-                check(trc_hip_add_f32(&a, &b, &d, nullptr), "add");
+                if (t->op == OP_ADD) {
+                    check(trc_hip_add_f32(&a, &b, &d, nullptr), "add");
+                } else {
+                    check(trc_hip_mul_f32(&a, &b, &d, nullptr), "mul");
+                }
+                return;
+            }
+            case OP_SUM: {
+                const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
+                const trc_hip_tensor d = describe(t, need_buffer(t));
+                check(trc_hip_sum_f32(&a, &d, nullptr), "sum");
+                return;
+            }
+            case OP_REPEAT: {
+                const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
+                const trc_hip_tensor d = describe(t, need_buffer(t));
+                check(trc_hip_repeat_f32(&a, &d, nullptr), "repeat");
                 return;
             }
             case OP_ACC: {

@@ -146,6 +146,40 @@ Tensor* add(Context* ctx, Tensor* a, Tensor* b) {
     return r;
 }
 
+// src/ops/trc_ops.cpp:59-61 (new_binary :19-32): a's shape, b broadcast to it.
+Tensor* mul(Context* ctx, Tensor* a, Tensor* b) {
+    TRC_CHECK(a != nullptr && b != nullptr, "mul: input is NULL");
+    TRC_CHECK(a->type == b->type, "mul: input types differ (%s vs %s)", type_name(a->type), type_name(b->type));
+    TRC_CHECK(tensor_are_same_shape(a, b) || tensor_can_repeat(b, a), "mul: b does not broadcast to a");
+    Tensor* r = new_tensor_nd(ctx, a->type, MAX_DIMS, a->ne);
+    r->op = OP_MUL;
+    r->src[0] = a;
+    r->src[1] = b;
+    r->nsrc = 2;
+    return r;
+}
+
+// src/ops/trc_ops.cpp:214-221: a one-element tensor of a's type.
+Tensor* sum(Context* ctx, Tensor* a) {
+    TRC_CHECK(a != nullptr, "sum: input is NULL");
+    Tensor* r = new_tensor_1d(ctx, a->type, 1);
+    r->op = OP_SUM;
+    r->src[0] = a;
+    r->nsrc = 1;
+    return r;
+}
+
+// src/ops/trc_ops.cpp:447-456: a broadcast (extent-1 dims) to target's shape.
+Tensor* repeat(Context* ctx, Tensor* a, Tensor* target) {
+    TRC_CHECK(a != nullptr && target != nullptr, "repeat: input is NULL");
+    TRC_CHECK(tensor_can_repeat(a, target), "repeat: a does not broadcast to target's shape");
+    Tensor* r = new_tensor_nd(ctx, a->type, MAX_DIMS, target->ne);
+    r->op = OP_REPEAT;
+    r->src[0] = a;
+    r->nsrc = 1;
+    return r;
+}
+
 Tensor* repeat_back(Context* ctx, Tensor* a, Tensor* b) {
     TRC_CHECK(a != nullptr && b != nullptr, "repeat_back: input is NULL");
     for (int i = 0; i < MAX_DIMS; ++i) {

@@ -319,6 +319,29 @@ int trc_hip_add_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_
     return launch_add_f32(*a, *b, *dst, (hipStream_t) stream);
 }
 
+int trc_hip_mul_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst, void* stream) {
+    TRC_FORCED("trc_hip_mul_f32");
+    if (a == nullptr || b == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_mul_f32: NULL tensor");
+    if (a->data == nullptr || b->data == nullptr || dst->data == nullptr) {
+        return fail(TRC_HIP_E_INVALID, "trc_hip_mul_f32: NULL data");
+    }
+    return launch_mul_f32(*a, *b, *dst, (hipStream_t) stream);
+}
+
+int trc_hip_repeat_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream) {
+    TRC_FORCED("trc_hip_repeat_f32");
+    if (a == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_repeat_f32: NULL tensor");
+    if (a->data == nullptr || dst->data == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_repeat_f32: NULL data");
+    return launch_repeat_f32(*a, *dst, (hipStream_t) stream);
+}
+
+int trc_hip_sum_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream) {
+    TRC_FORCED("trc_hip_sum_f32");
+    if (a == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_sum_f32: NULL tensor");
+    if (a->data == nullptr || dst->data == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_sum_f32: NULL data");
+    return launch_sum_f32(*a, *dst, (hipStream_t) stream);
+}
+
 int trc_hip_acc_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst, size_t nb1,
                     size_t nb2, size_t nb3, size_t offset, int inplace, void* stream) {
     TRC_FORCED("trc_hip_acc_f32");

@@ -1,12 +1,16 @@
-// F32 element-wise graph ops the autograd of mul_mat needs on the device
-// (row f2 of the hot-path scope): ADD with ggml broadcast, ACC into a strided
-// region, REPEAT_BACK. Each output element is produced by the same single
-// float operation, or the same ordered sum, as the reference CPU kernels, so
-// the results are bit-identical:
-//   add          src/ops/trc_ops.cpp:19-32,46; compute_binary
+// F32 element-wise graph ops that a Linear layer's forward and autograd
+// backward put around mul_mat on the device: ADD and MUL with ggml broadcast,
+// ACC into a strided region, REPEAT_BACK, REPEAT, and SUM (the scalar loss).
+// Each output element is produced by the same single float operation, or the
+// same ordered sum, as the reference CPU kernels, so the results are
+// bit-identical:
+//   add, mul     src/ops/trc_ops.cpp:19-32,46,59; compute_binary
 //                src/backends/cpu/trc_cpu_ops.cpp:52-78 (offset_broadcast :18-28)
 //   acc          src/core/trc_tensor.cpp:322-361; compute_acc trc_cpu_ops.cpp:954-999
 //   repeat_back  src/ops/trc_ops.cpp:458-470; compute_repeat_back trc_cpu_ops.cpp:932-952
+//   repeat       src/ops/trc_ops.cpp:447-456; compute_repeat trc_cpu_ops.cpp:913-928
+//   sum          src/ops/trc_ops.cpp:214-221; compute_sum trc_cpu_ops.cpp:302-315
+//                (row_sum_f32 :284-300)
 //
 // Mapping: one workgroup row-loop per ggml row (ne0-run); lanes stride over the
 // row, so loads and stores along ne0 are coalesced whenever nb0 == 4.
@@ -31,10 +35,13 @@ Shape4 shape_of(const trc_hip_tensor& t) {
     return s;
 }
 
-// dst[i] = a[i] + b[broadcast(i)], rows of dst distributed over the grid
-__global__ __launch_bounds__(EW_THREADS) void k_add(const uint8_t* __restrict__ a, Shape4 sa,
-                                                    const uint8_t* __restrict__ b, Shape4 sb, uint8_t* __restrict__ d,
-                                                    Shape4 sd) {
+enum class BinOp { ADD, MUL };
+
+// dst[i] = a[i] (+ or *) b[broadcast(i)], rows of dst distributed over the grid
+template <BinOp OP>
+__global__ __launch_bounds__(EW_THREADS) void k_binary(const uint8_t* __restrict__ a, Shape4 sa,
+                                                       const uint8_t* __restrict__ b, Shape4 sb,
+                                                       uint8_t* __restrict__ d, Shape4 sd) {
     const int64_t rows = sd.ne[1] * sd.ne[2] * sd.ne[3];
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const int64_t i1 = r % sd.ne[1], i2 = (r / sd.ne[1]) % sd.ne[2], i3 = r / (sd.ne[1] * sd.ne[2]);
@@ -44,9 +51,57 @@ __global__ __launch_bounds__(EW_THREADS) void k_add(const uint8_t* __restrict__ 
         uint8_t* pd = d + i1 * sd.nb[1] + i2 * sd.nb[2] + i3 * sd.nb[3];
         const int64_t bnb0 = sb.ne[0] == 1 ? 0 : sb.nb[0];
         for (int64_t i0 = threadIdx.x; i0 < sd.ne[0]; i0 += EW_THREADS) {
-            *(float*) (pd + i0 * sd.nb[0]) = *(const float*) (pa + i0 * sa.nb[0]) + *(const float*) (pb + i0 * bnb0);
+            const float va = *(const float*) (pa + i0 * sa.nb[0]), vb = *(const float*) (pb + i0 * bnb0);
+            *(float*) (pd + i0 * sd.nb[0]) = OP == BinOp::ADD ? va + vb : va * vb;
         }
     }
+}
+
+// dst[i] = a[i mod a.ne, per dim]: every dim of a is 1 (broadcast) or dst's
+// extent; one thread per dst element, grid-stride
+__global__ __launch_bounds__(EW_THREADS) void k_repeat(const uint8_t* __restrict__ a, Shape4 sa,
+                                                       uint8_t* __restrict__ d, Shape4 sd) {
+    const int64_t n = sd.ne[0] * sd.ne[1] * sd.ne[2] * sd.ne[3];
+    for (int64_t j = (int64_t) blockIdx.x * EW_THREADS + threadIdx.x; j < n; j += (int64_t) gridDim.x * EW_THREADS) {
+        int64_t rem = j, oa = 0, od = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t idx = rem % sd.ne[k];
+            rem /= sd.ne[k];
+            oa += (sa.ne[k] == 1 ? 0 : idx % sa.ne[k]) * sa.nb[k];
+            od += idx * sd.nb[k];
+        }
+        *(float*) (d + od) = *(const float*) (a + oa);
+    }
+}
+
+// *d = sum of a, as compute_sum forms it: each row (ne0-run) summed from 0 in
+// double in element order, the row sums added in double in row order (i1
+// fastest, then i2, i3), one rounding to float at the end. One workgroup: each
+// thread sums one row of a block of SUM_THREADS rows into LDS, then thread 0
+// adds the block's row sums in order.
+constexpr int SUM_THREADS = 1024;
+__global__ __launch_bounds__(SUM_THREADS) void k_sum(const uint8_t* __restrict__ a, Shape4 sa, float* __restrict__ d) {
+    __shared__ double row[SUM_THREADS];
+    const int64_t rows = sa.ne[1] * sa.ne[2] * sa.ne[3];
+    double total = 0.0;
+    for (int64_t r0 = 0; r0 < rows; r0 += SUM_THREADS) {
+        const int64_t r = r0 + threadIdx.x;
+        double s = 0.0;
+        if (r < rows) {
+            const int64_t i1 = r % sa.ne[1], i2 = (r / sa.ne[1]) % sa.ne[2], i3 = r / (sa.ne[1] * sa.ne[2]);
+            const uint8_t* p = a + i1 * sa.nb[1] + i2 * sa.nb[2] + i3 * sa.nb[3];
+            for (int64_t i0 = 0; i0 < sa.ne[0]; ++i0) s = s + (double) *(const float*) (p + i0 * sa.nb[0]);
+        }
+        row[threadIdx.x] = s;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int64_t n = rows - r0 < SUM_THREADS ? rows - r0 : SUM_THREADS;
+            for (int64_t k = 0; k < n; ++k) total = total + row[k];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *d = (float) total;
 }
 
 // contiguous copy of n floats (acc with inplace == false starts from a)
@@ -128,23 +183,56 @@ bool shape_ok(const trc_hip_tensor& t) {
     return true;
 }
 
+template <BinOp OP>
+int launch_binary(const char* name, const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d,
+                  hipStream_t s) {
+    if (a.type != TRC_HIP_TYPE_F32 || b.type != TRC_HIP_TYPE_F32 || d.type != TRC_HIP_TYPE_F32) {
+        return fail(TRC_HIP_E_INVALID, "%s: F32 tensors only", name);
+    }
+    if (!shape_ok(a) || !shape_ok(b) || !shape_ok(d)) return fail(TRC_HIP_E_SHAPE, "%s: empty or negative extent", name);
+    for (int k = 0; k < 4; ++k) {
+        if (d.ne[k] != a.ne[k] || (b.ne[k] != a.ne[k] && b.ne[k] != 1)) {
+            return fail(TRC_HIP_E_SHAPE, "%s: dst must have a's shape and b must broadcast to it (dim %d)", name, k);
+        }
+    }
+    if (!f32_aligned(a) || !f32_aligned(b) || !f32_aligned(d)) return fail(TRC_HIP_E_ALIGN, "%s: 4-byte alignment", name);
+    const int64_t rows = d.ne[1] * d.ne[2] * d.ne[3];
+    hipLaunchKernelGGL(k_binary<OP>, dim3(grid_for(rows, 1)), dim3(EW_THREADS), 0, s, (const uint8_t*) a.data,
+                       shape_of(a), (const uint8_t*) b.data, shape_of(b), (uint8_t*) d.data, shape_of(d));
+    return check_launch(name);
+}
+
 }  // namespace
 
 int launch_add_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t s) {
-    if (a.type != TRC_HIP_TYPE_F32 || b.type != TRC_HIP_TYPE_F32 || d.type != TRC_HIP_TYPE_F32) {
-        return fail(TRC_HIP_E_INVALID, "add: F32 tensors only");
-    }
-    if (!shape_ok(a) || !shape_ok(b) || !shape_ok(d)) return fail(TRC_HIP_E_SHAPE, "add: empty or negative extent");
+    return launch_binary<BinOp::ADD>("add", a, b, d, s);
+}
+
+int launch_mul_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t s) {
+    return launch_binary<BinOp::MUL>("mul", a, b, d, s);
+}
+
+int launch_repeat_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t s) {
+    if (a.type != TRC_HIP_TYPE_F32 || d.type != TRC_HIP_TYPE_F32) return fail(TRC_HIP_E_INVALID, "repeat: F32 tensors only");
+    if (!shape_ok(a) || !shape_ok(d)) return fail(TRC_HIP_E_SHAPE, "repeat: empty or negative extent");
     for (int k = 0; k < 4; ++k) {
-        if (d.ne[k] != a.ne[k] || (b.ne[k] != a.ne[k] && b.ne[k] != 1)) {
-            return fail(TRC_HIP_E_SHAPE, "add: dst must have a's shape and b must broadcast to it (dim %d)", k);
-        }
+        // ggml_can_repeat(a, dst): every dst extent a multiple of a's
+        if (d.ne[k] % a.ne[k] != 0) return fail(TRC_HIP_E_SHAPE, "repeat: dst.ne[%d] is not a multiple of a.ne[%d]", k, k);
     }
-    if (!f32_aligned(a) || !f32_aligned(b) || !f32_aligned(d)) return fail(TRC_HIP_E_ALIGN, "add: 4-byte alignment");
-    const int64_t rows = d.ne[1] * d.ne[2] * d.ne[3];
-    hipLaunchKernelGGL(k_add, dim3(grid_for(rows, 1)), dim3(EW_THREADS), 0, s, (const uint8_t*) a.data, shape_of(a),
-                       (const uint8_t*) b.data, shape_of(b), (uint8_t*) d.data, shape_of(d));
-    return check_launch("add");
+    if (!f32_aligned(a) || !f32_aligned(d)) return fail(TRC_HIP_E_ALIGN, "repeat: 4-byte alignment");
+    const int64_t n = nelem(d);
+    hipLaunchKernelGGL(k_repeat, dim3(grid_for(n, EW_THREADS)), dim3(EW_THREADS), 0, s, (const uint8_t*) a.data,
+                       shape_of(a), (uint8_t*) d.data, shape_of(d));
+    return check_launch("repeat");
+}
+
+int launch_sum_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t s) {
+    if (a.type != TRC_HIP_TYPE_F32 || d.type != TRC_HIP_TYPE_F32) return fail(TRC_HIP_E_INVALID, "sum: F32 tensors only");
+    if (!shape_ok(a) || !shape_ok(d)) return fail(TRC_HIP_E_SHAPE, "sum: empty or negative extent");
+    if (nelem(d) != 1) return fail(TRC_HIP_E_SHAPE, "sum: dst must hold one element");
+    if (!f32_aligned(a) || !f32_aligned(d)) return fail(TRC_HIP_E_ALIGN, "sum: 4-byte alignment");
+    hipLaunchKernelGGL(k_sum, dim3(1), dim3(SUM_THREADS), 0, s, (const uint8_t*) a.data, shape_of(a), (float*) d.data);
+    return check_launch("sum");
 }
 
 int launch_acc_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, size_t nb1, size_t nb2,

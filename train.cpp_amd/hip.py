@@ -24,6 +24,7 @@ EXPORTS = (
     "trc_hip_malloc", "trc_hip_free", "trc_hip_h2d", "trc_hip_d2h", "trc_hip_memset",
     "trc_hip_fill_f32", "trc_hip_dequant", "trc_hip_mul_mat_f32", "trc_hip_qmatvec", "trc_hip_cpy",
     "trc_hip_add_f32", "trc_hip_acc_f32", "trc_hip_repeat_back_f32", "trc_hip_qmatvec_noalloc",
+    "trc_hip_mul_f32", "trc_hip_repeat_f32", "trc_hip_sum_f32",
 )
 
 
@@ -97,6 +98,9 @@ def load() -> C.CDLL:
         "trc_hip_add_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_acc_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), SZ, SZ, SZ, SZ, I, P], I),
         "trc_hip_repeat_back_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), P], I),
+        "trc_hip_mul_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
+        "trc_hip_repeat_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), P], I),
+        "trc_hip_sum_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), P], I),
     }
     for name, (args, ret) in sig.items():
         fn = getattr(lib, name)
@@ -167,6 +171,18 @@ def acc_f32(a: Tensor, b: Tensor, d: Tensor, nb1: int, nb2: int, nb3: int, offse
 
 def repeat_back_f32(a: Tensor, d: Tensor, stream: int | None = None) -> None:
     check(load().trc_hip_repeat_back_f32(C.byref(a), C.byref(d), stream))
+
+
+def mul_f32(a: Tensor, b: Tensor, d: Tensor, stream: int | None = None) -> None:
+    check(load().trc_hip_mul_f32(C.byref(a), C.byref(b), C.byref(d), stream))
+
+
+def repeat_f32(a: Tensor, d: Tensor, stream: int | None = None) -> None:
+    check(load().trc_hip_repeat_f32(C.byref(a), C.byref(d), stream))
+
+
+def sum_f32(a: Tensor, d: Tensor, stream: int | None = None) -> None:
+    check(load().trc_hip_sum_f32(C.byref(a), C.byref(d), stream))
 
 
 def fill_f32(ptr: int, value: float, count: int, stream: int | None = None) -> None:
