@@ -6,8 +6,8 @@
 // With the HIP backend the legacy quant formats are dequantized on the GPU:
 // gguf_load_tensor into an F32 tensor of a HIP buffer uploads the raw blocks
 // and dequantizes in place (no host F32 copy); gguf_tensor_to_f32 stages
-// through the GPU too and needs a HIP device. The writer side is not part of
-// this backend.
+// through the GPU when one is visible and dequantizes on the host otherwise
+// (the same bits either way). The writer side is not part of this backend.
 #pragma once
 
 #include "trc_context.h"
@@ -45,14 +45,31 @@ int64_t     gguf_kv_count(const GgufFile* f);
 int64_t     gguf_find_key(const GgufFile* f, const char* key);
 const char* gguf_key(const GgufFile* f, int64_t index);
 GgufType    gguf_kv_type(const GgufFile* f, int64_t index);
+GgufType    gguf_arr_type(const GgufFile* f, int64_t index);
+int64_t     gguf_arr_count(const GgufFile* f, int64_t index);
 bool        gguf_has_key(const GgufFile* f, const char* key);
+
+// Scalars: a missing key or another type logs an error and returns 0 (nullptr
+// for strings). BOOL is one byte on disk.
+uint8_t     gguf_get_u8(const GgufFile* f, const char* key);
+int8_t      gguf_get_i8(const GgufFile* f, const char* key);
+uint16_t    gguf_get_u16(const GgufFile* f, const char* key);
+int16_t     gguf_get_i16(const GgufFile* f, const char* key);
 uint32_t    gguf_get_u32(const GgufFile* f, const char* key);
 int32_t     gguf_get_i32(const GgufFile* f, const char* key);
 uint64_t    gguf_get_u64(const GgufFile* f, const char* key);
 int64_t     gguf_get_i64(const GgufFile* f, const char* key);
 float       gguf_get_f32(const GgufFile* f, const char* key);
 bool        gguf_get_bool(const GgufFile* f, const char* key);
+double      gguf_get_f64(const GgufFile* f, const char* key);
 const char* gguf_get_str(const GgufFile* f, const char* key);
+
+// Arrays: a missing key, another element type or an index out of range logs an
+// error and returns nullptr.
+const int32_t* gguf_get_arr_i32(const GgufFile* f, const char* key, int64_t* n);
+const int64_t* gguf_get_arr_i64(const GgufFile* f, const char* key, int64_t* n);
+const float*   gguf_get_arr_f32(const GgufFile* f, const char* key, int64_t* n);
+const char*    gguf_get_arr_str(const GgufFile* f, const char* key, int64_t index);
 
 int64_t               gguf_tensor_count(const GgufFile* f);
 int64_t               gguf_find_tensor(const GgufFile* f, const char* name);

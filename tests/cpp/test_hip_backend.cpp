@@ -552,12 +552,13 @@ void test_fill_and_unsupported(Device* dev) {
     for (float v : vb) ok = ok && v == -3.0f;
     EXPECT(ok);
     // nodes the backend does not implement are reported, not run
-    Tensor* mul_node = new_tensor_2d(ctx, TYPE_F32, 1000, 3);
-    mul_node->op = OP_MUL;
-    mul_node->src[0] = a;
-    mul_node->src[1] = a;
-    mul_node->nsrc = 2;
-    EXPECT(!dev->supports_op(mul_node));
+    Tensor* div_node = new_tensor_2d(ctx, TYPE_F32, 1000, 3);
+    div_node->op = OP_DIV;
+    div_node->src[0] = a;
+    div_node->src[1] = a;
+    div_node->nsrc = 2;
+    EXPECT(!dev->supports_op(div_node));
+    EXPECT(dev->supports_op(mul(ctx, a, a)));
     EXPECT(dev->supports_op(add(ctx, a, a)));
     Tensor* r2 = new_tensor_2d(ctx, TYPE_F32, 4, 2);
     EXPECT(!dev->supports_op(acc(ctx, a, r2, 4, 0, 0, 0, false)));  // the region's rows overlap
@@ -565,8 +566,8 @@ void test_fill_and_unsupported(Device* dev) {
     Tensor* hh = mul_mat(ctx, h, h);  // F16 mul_mat: not on this backend
     EXPECT(!dev->supports_op(hh));
     Graph* g = graph_new(ctx);
-    graph_build_forward_expand(ctx, g, mul_node);
-    EXPECT(graph_first_unsupported(g, dev) == mul_node);
+    graph_build_forward_expand(ctx, g, div_node);
+    EXPECT(graph_first_unsupported(g, dev) == div_node);
     std::printf("    [%s] fill + unsupported-op reporting\n", ok ? " OK " : "FAIL");
     buffer_free(buf);
     EXPECT(a->data == nullptr && a->buffer == nullptr);  // buffer_free detaches its tensors
@@ -646,6 +647,265 @@ void test_core_cpu(const std::string& dir) {
     std::printf("    [%s] layout, views, graph order, GGUF parsing\n", g_failures == 0 ? " OK " : "FAIL");
 }
 
+// GGUF bytes assembled field by field (little-endian), for files the reader
+// must accept or reject.
+struct GgufBytes {
+    std::vector<uint8_t> v;
+    void header(uint64_t n_tensors, uint64_t n_kv, uint32_t version = 3) {
+        put(v, "GGUF", 4);
+        put<uint32_t>(v, version);
+        put<uint64_t>(v, n_tensors);
+        put<uint64_t>(v, n_kv);
+    }
+    void str(const std::string& s) {
+        put<uint64_t>(v, s.size());
+        put(v, s.data(), s.size());
+    }
+    template <typename T>
+    void kv(const std::string& key, GgufType t, T x) {
+        str(key);
+        put<int32_t>(v, (int32_t) t);
+        put<T>(v, x);
+    }
+    void kv_str(const std::string& key, const std::string& x) {
+        str(key);
+        put<int32_t>(v, (int32_t) GgufType::STRING);
+        str(x);
+    }
+    template <typename T>
+    void kv_arr(const std::string& key, GgufType et, const std::vector<T>& xs) {
+        str(key);
+        put<int32_t>(v, (int32_t) GgufType::ARRAY);
+        put<int32_t>(v, (int32_t) et);
+        put<uint64_t>(v, xs.size());
+        for (const T& x : xs) put<T>(v, x);
+    }
+    void kv_arr_str(const std::string& key, const std::vector<std::string>& xs) {
+        str(key);
+        put<int32_t>(v, (int32_t) GgufType::ARRAY);
+        put<int32_t>(v, (int32_t) GgufType::STRING);
+        put<uint64_t>(v, xs.size());
+        for (const std::string& x : xs) str(x);
+    }
+    void tensor(const std::string& name, Type type, const std::vector<int64_t>& ne, uint64_t offset) {
+        str(name);
+        put<uint32_t>(v, (uint32_t) ne.size());
+        for (int64_t d : ne) put<int64_t>(v, d);
+        put<uint32_t>(v, (uint32_t) type);
+        put<uint64_t>(v, offset);
+    }
+    void pad32() {
+        while (v.size() % 32) v.push_back(0);
+    }
+    void f32_ramp(int n) {
+        for (int i = 0; i < n; ++i) put<float>(v, (float) i);
+    }
+    void zeros(size_t n) { v.insert(v.end(), n, 0); }
+    bool write(const std::string& path) const {
+        FILE* fp = std::fopen(path.c_str(), "wb");
+        if (!fp) return false;
+        const bool ok = std::fwrite(v.data(), 1, v.size(), fp) == v.size();
+        std::fclose(fp);
+        return ok;
+    }
+};
+
+// One F32 tensor "w" of 8 elements 0..7 (the valid file of tests/test_gguf.cpp:566-578).
+GgufBytes valid_f32_file() {
+    GgufBytes b;
+    b.header(1, 0);
+    b.tensor("w", TYPE_F32, {8}, 0);
+    b.pad32();
+    b.f32_ramp(8);
+    b.pad32();
+    return b;
+}
+
+// The reference's GGUF reader tests (tests/test_gguf.cpp:135-229 metadata
+// round trip, :448-525 metadata-only and validation, :526-635 corrupt files)
+// against this repository's reader, on files assembled byte by byte (the
+// reader side has no writer), and the host dequantization gguf_tensor_to_f32
+// falls back to without a GPU, bit for bit against the oracle.
+void test_gguf_reader_cpu(const std::string& dir) {
+    std::printf("GGUF reader (no device)\n");
+    const int before = g_failures;
+    const std::string path = dir + "/reader.gguf";
+
+    // metadata round trip: every scalar type, a UTF-8 string, four array kinds
+    {
+        GgufBytes b;
+        b.header(0, 17);
+        b.kv_str("general.architecture", "traincpp.test");
+        b.kv<uint8_t>("t.u8", GgufType::U8, 200);
+        b.kv<int8_t>("t.i8", GgufType::I8, -100);
+        b.kv<uint16_t>("t.u16", GgufType::U16, 60000);
+        b.kv<int16_t>("t.i16", GgufType::I16, -30000);
+        b.kv<uint32_t>("t.u32", GgufType::U32, 7u);
+        b.kv<int32_t>("t.i32", GgufType::I32, -2000000000);
+        b.kv<float>("t.f32", GgufType::F32, 3.25f);
+        b.kv<uint8_t>("t.bool", GgufType::BOOL, 1);
+        b.kv<uint64_t>("t.u64", GgufType::U64, 12345678901234567890ull);
+        b.kv<int64_t>("t.i64", GgufType::I64, -1234567890123456789ll);
+        b.kv<double>("t.f64", GgufType::F64, 2.5);
+        b.kv_str("t.str", "\xe4\xb8\xad\xe6\x96\x87 UTF-8 / ascii");
+        b.kv_arr<int32_t>("t.arr_i32", GgufType::I32, {1, -2, 3});
+        b.kv_arr<float>("t.arr_f32", GgufType::F32, {0.5f, -1.5f});
+        b.kv_arr<int64_t>("t.arr_i64", GgufType::I64, {1, -5, 1099511627776ll});
+        b.kv_arr_str("t.arr_str", {"alpha", "\xe8\xb4\x9d\xe5\xa1\x94"});
+        b.pad32();
+        EXPECT(b.write(path));
+        GgufFile* f = gguf_open(path.c_str(), true);
+        EXPECT(f != nullptr);
+        if (f != nullptr) {
+            EXPECT(gguf_version(f) == 3 && gguf_alignment(f) == 32 && gguf_kv_count(f) == 17);
+            EXPECT(gguf_get_u8(f, "t.u8") == 200 && gguf_get_i8(f, "t.i8") == -100);
+            EXPECT(gguf_get_u16(f, "t.u16") == 60000 && gguf_get_i16(f, "t.i16") == -30000);
+            EXPECT(gguf_get_u32(f, "t.u32") == 7 && gguf_get_i32(f, "t.i32") == -2000000000);
+            EXPECT(gguf_get_f32(f, "t.f32") == 3.25f && gguf_get_bool(f, "t.bool"));
+            EXPECT(gguf_get_u64(f, "t.u64") == 12345678901234567890ull);
+            EXPECT(gguf_get_i64(f, "t.i64") == -1234567890123456789ll && gguf_get_f64(f, "t.f64") == 2.5);
+            EXPECT(std::string(gguf_get_str(f, "t.str")) == "\xe4\xb8\xad\xe6\x96\x87 UTF-8 / ascii");
+            EXPECT(std::string(gguf_get_str(f, "general.architecture")) == "traincpp.test");
+            EXPECT(gguf_has_key(f, "t.u8") && !gguf_has_key(f, "t.nope"));
+            int64_t n = 0;
+            const int32_t* p32 = gguf_get_arr_i32(f, "t.arr_i32", &n);
+            EXPECT(p32 != nullptr && n == 3 && p32[0] == 1 && p32[1] == -2 && p32[2] == 3);
+            const float* pf = gguf_get_arr_f32(f, "t.arr_f32", &n);
+            EXPECT(pf != nullptr && n == 2 && pf[0] == 0.5f && pf[1] == -1.5f);
+            const int64_t* p64 = gguf_get_arr_i64(f, "t.arr_i64", &n);
+            EXPECT(p64 != nullptr && n == 3 && p64[0] == 1 && p64[1] == -5 && p64[2] == 1099511627776ll);
+            EXPECT(std::string(gguf_get_arr_str(f, "t.arr_str", 1)) == "\xe8\xb4\x9d\xe5\xa1\x94");
+            EXPECT(gguf_get_arr_str(f, "t.arr_str", 2) == nullptr);       // index out of range
+            EXPECT(gguf_get_arr_i32(f, "t.arr_f32", &n) == nullptr);     // wrong element type
+            EXPECT(gguf_get_u32(f, "t.i32") == 0);                       // wrong scalar type
+            const int64_t idx = gguf_find_key(f, "t.arr_str");
+            EXPECT(idx >= 0 && gguf_kv_type(f, idx) == GgufType::ARRAY && gguf_arr_type(f, idx) == GgufType::STRING &&
+                   gguf_arr_count(f, idx) == 2 && std::string(gguf_key(f, idx)) == "t.arr_str");
+            gguf_close(f);
+        }
+    }
+
+    // metadata only: no data access; with data: the values
+    {
+        EXPECT(valid_f32_file().write(path));
+        GgufFile* f = gguf_open(path.c_str(), false);
+        EXPECT(f != nullptr && gguf_tensor_count(f) == 1);
+        std::vector<float> got(8, -1.f);
+        if (f != nullptr) {
+            EXPECT(!gguf_tensor_to_f32(f, "w", got.data(), 8));
+            gguf_close(f);
+        }
+        f = gguf_open(path.c_str(), true);
+        EXPECT(f != nullptr);
+        if (f != nullptr) {
+            EXPECT(gguf_tensor_to_f32(f, "w", got.data(), 8));
+            for (int i = 0; i < 8; ++i) EXPECT(got[(size_t) i] == (float) i);
+            gguf_close(f);
+        }
+    }
+
+    // validate: valid, bad magic, truncated data, missing file
+    {
+        GgufBytes b = valid_f32_file();
+        EXPECT(b.write(path) && gguf_validate(path.c_str()));
+        GgufBytes bad = b;
+        bad.v[0] = 'X';
+        EXPECT(bad.write(path) && !gguf_validate(path.c_str()));
+        EXPECT(b.write(path));
+        GgufFile* f = gguf_open(path.c_str(), true);
+        const size_t data_off = f != nullptr ? gguf_data_offset(f) : 0;
+        gguf_close(f);
+        bad = b;
+        bad.v.resize(data_off + 4);  // 4 of the tensor's 32 bytes
+        EXPECT(bad.write(path) && !gguf_validate(path.c_str()));
+        std::remove(path.c_str());
+        EXPECT(!gguf_validate(path.c_str()));
+    }
+
+    // corrupt files are rejected (test_gguf.cpp:526-635, all ten cases)
+    {
+        std::vector<std::pair<const char*, GgufBytes>> bad;
+        GgufBytes v = valid_f32_file();
+        v.v[0] = 'X';
+        bad.push_back({"bad magic", v});
+        v = valid_f32_file();
+        v.v[4] = 1;
+        bad.push_back({"version 1", v});
+        v = valid_f32_file();
+        v.v[4] = 4;
+        bad.push_back({"version 4", v});
+        GgufBytes b;
+        b.header(1, 0);
+        b.tensor("w", TYPE_F32, {8}, 0);
+        bad.push_back({"data section missing", b});
+        b = GgufBytes();
+        b.header(2, 0);
+        b.tensor("w", TYPE_F32, {8}, 0);
+        b.tensor("w", TYPE_F32, {8}, 32);
+        b.pad32();
+        b.zeros(64);
+        b.pad32();
+        bad.push_back({"duplicate tensor name", b});
+        b = GgufBytes();
+        b.header(2, 0);
+        b.tensor("a", TYPE_F32, {8}, 0);
+        b.tensor("b", TYPE_F32, {8}, 0);  // should be 32
+        b.pad32();
+        b.zeros(64);
+        b.pad32();
+        bad.push_back({"offsets not contiguous", b});
+        b = GgufBytes();
+        b.header(1, 0);
+        b.tensor("w", TYPE_IQ2_XXS, {256}, 0);
+        b.pad32();
+        b.zeros(66);
+        b.pad32();
+        bad.push_back({"type not implemented (IQ2_XXS)", b});
+        b = GgufBytes();
+        b.header(1, 0);
+        b.tensor("w", TYPE_Q4_0, {30}, 0);
+        b.pad32();
+        b.zeros(18);
+        b.pad32();
+        bad.push_back({"ne0 not a whole number of blocks", b});
+        b = GgufBytes();
+        b.header(0, 2);
+        b.kv<uint32_t>("k", GgufType::U32, 1);
+        b.kv<uint32_t>("k", GgufType::U32, 2);
+        b.pad32();
+        bad.push_back({"duplicate key", b});
+        for (auto& [what, bytes] : bad) {
+            EXPECT(bytes.write(path));
+            GgufFile* f = gguf_open(path.c_str(), true);
+            if (f != nullptr) {
+                std::printf("    accepted a corrupt file: %s\n", what);
+                ++g_failures;
+                gguf_close(f);
+            }
+        }
+        std::remove(path.c_str());
+        EXPECT(gguf_open((dir + "/missing.gguf").c_str(), true) == nullptr);
+    }
+
+    // gguf_tensor_to_f32 of every legacy format, bit for bit against the oracle
+    // (on the host when no GPU is visible, through the GPU otherwise)
+    for (Type qt : {TYPE_Q4_0, TYPE_Q4_1, TYPE_Q5_0, TYPE_Q5_1, TYPE_Q8_0}) {
+        const std::vector<uint8_t> blocks = quant_blocks(qt, 96, 40 + (uint64_t) qt);
+        EXPECT(write_gguf(path, "w", qt, {32 * 12, 8}, blocks));
+        GgufFile* f = gguf_open(path.c_str(), true);
+        EXPECT(f != nullptr);
+        if (f == nullptr) continue;
+        std::vector<float> got(96 * 32);
+        EXPECT(gguf_tensor_to_f32(f, "w", got.data(), (int64_t) got.size()));
+        const std::vector<float> want = oracle_dequant(qt, blocks);
+        EXPECT(std::memcmp(got.data(), want.data(), got.size() * 4) == 0);
+        gguf_close(f);
+    }
+    std::remove(path.c_str());
+    std::printf("    [%s] metadata round trip, metadata-only, validate, 10 corrupt files, dequant to F32\n",
+                g_failures == before ? " OK " : "FAIL");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -658,6 +918,7 @@ int main(int argc, char** argv) {
         return 0;
     }
     test_core_cpu(dir);
+    test_gguf_reader_cpu(dir);
     if (mode != "--cpu") {
         Device* dev = device_by_type(DeviceType::GPU);
         if (dev == nullptr) {

@@ -34,9 +34,11 @@ def test_mul_mat_shape_guard_aborts():
 @pytest.mark.skipif(not (REFERENCE_INCLUDE / "traincpp" / "trc_backend.h").exists(),
                     reason="reference checkout not present")
 def test_hip_device_compiles_against_reference_headers(tmp_path):
+    # the plugin's own two headers beside the reference's (what a maintainer copies)
     abi = tmp_path / "abi"
-    abi.mkdir()
+    (abi / "traincpp").mkdir(parents=True)
     shutil.copy(ROOT / "include" / "trc_hip_abi.h", abi)
+    shutil.copy(ROOT / "include" / "traincpp" / "trc_hip.h", abi / "traincpp")
     r = subprocess.run(["g++", "-std=c++20", "-fsyntax-only", "-Wall", "-Wextra", "-Wno-unused-parameter",
                         f"-I{REFERENCE_INCLUDE}", f"-I{abi}",
                         str(ROOT / "train.cpp_amd" / "csrc" / "backend" / "hip_device.cpp")],

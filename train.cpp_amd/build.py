@@ -38,7 +38,8 @@ HIP_FLAGS = [
 HIP_FILE_FLAGS = {"dequant.hip": ["-ffp-contract=off"]}
 
 CXX = os.environ.get("CXX", "g++")
-CXX_FLAGS = ["-O2", "-std=c++20", "-fPIC", f"-I{INCLUDE}", f"-I{CORE_SRC}", "-Wall", "-Wextra",
+# -ffp-contract=off: the host dequantizer (core/gguf.cpp) rounds d*q and +m on their own.
+CXX_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-ffp-contract=off", f"-I{INCLUDE}", f"-I{CORE_SRC}", "-Wall", "-Wextra",
              "-Wno-unused-parameter"]
 
 

@@ -10,7 +10,13 @@
 // aborts with a diagnostic. This file uses only the public traincpp API and
 // the C ABI, so it compiles against the reference's own headers as well.
 #include "traincpp/traincpp.h"
+#include "traincpp/trc_hip.h"
 #include "trc_hip_abi.h"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include <cstdint>
 #include <cstdio>
@@ -479,7 +485,10 @@ Device* hip_device(int ordinal) {
 
 bool hip_dequant_into(Tensor* dst, Type type, const void* host_blocks, int64_t n_blocks) {
     HipBuffer* buf = hip_buffer_of(dst);
-    if (buf == nullptr) return false;
+    if (buf == nullptr || !legacy_quant(type) || dst->type != TYPE_F32 || !tensor_is_contiguous(dst) ||
+        tensor_nelements(dst) != n_blocks * 32) {
+        return false;
+    }
     HipDevice* dev = static_cast<HipDevice*>(buf->buffer_type()->device());
     dev->select();
     const size_t raw = (size_t) n_blocks * type_size(type);
@@ -489,6 +498,48 @@ bool hip_dequant_into(Tensor* dst, Type type, const void* host_blocks, int64_t n
           "gguf_load_tensor (dequantize)");
     check(trc_hip_sync(nullptr), "gguf_load_tensor");
     return true;
+}
+
+bool hip_gguf_load_tensor(const char* path, const GgufFile* f, const char* name, Tensor* dst) {
+    if (path == nullptr || f == nullptr || name == nullptr || dst == nullptr) return false;
+    const int64_t idx = gguf_find_tensor(f, name);
+    if (idx < 0) {
+        std::fprintf(stderr, "[traincpp-hip][ERROR] hip_gguf_load_tensor: no tensor named %s\n", name);
+        return false;
+    }
+    const GgufTensorInfo* info = gguf_tensor_info(f, idx);
+    const int64_t n = gguf_tensor_nelements(f, idx);
+    if (!legacy_quant(info->type) || dst->type != TYPE_F32 || !tensor_is_contiguous(dst) ||
+        tensor_nelements(dst) != n || hip_buffer_of(dst) == nullptr) {
+        return false;
+    }
+    const int64_t n_blocks = n / 32;
+    const size_t bytes = (size_t) n_blocks * type_size(info->type);
+    const size_t off = gguf_data_offset(f) + info->offset;
+    const int fd = ::open(path, O_RDONLY);
+    if (fd < 0) {
+        std::fprintf(stderr, "[traincpp-hip][ERROR] hip_gguf_load_tensor: cannot open %s\n", path);
+        return false;
+    }
+    struct stat st;
+    if (::fstat(fd, &st) != 0 || off + bytes > (size_t) st.st_size) {
+        ::close(fd);
+        std::fprintf(stderr, "[traincpp-hip][ERROR] hip_gguf_load_tensor: %s is shorter than tensor %s needs\n", path,
+                     name);
+        return false;
+    }
+    const size_t page = (size_t) ::sysconf(_SC_PAGESIZE);
+    const size_t lead = off % page;
+    void* m = ::mmap(nullptr, lead + bytes, PROT_READ, MAP_PRIVATE, fd, (off_t) (off - lead));
+    ::close(fd);
+    if (m == MAP_FAILED) {
+        std::fprintf(stderr, "[traincpp-hip][ERROR] hip_gguf_load_tensor: mmap of %s failed\n", path);
+        return false;
+    }
+    ::madvise(m, lead + bytes, MADV_SEQUENTIAL);
+    const bool ok = hip_dequant_into(dst, info->type, (const uint8_t*) m + lead, n_blocks);
+    ::munmap(m, lead + bytes);
+    return ok;
 }
 
 bool hip_dequant_host(Type type, const void* host_blocks, int64_t n_blocks, float* out) {

@@ -27,6 +27,8 @@ struct GgufKvEntry {
     std::string str;
     GgufType    arr_type = GgufType::U8;
     uint64_t    arr_n = 0;
+    std::vector<uint64_t>    arr_words;  // scalar array payload, 8-byte aligned copy
+    std::vector<std::string> arr_strs;   // string array payload
 };
 
 struct GgufFile {
@@ -96,15 +98,19 @@ bool read_kv(Reader& r, GgufKvEntry& kv) {
             kv.arr_type = (GgufType) et;
             if (!r.get(kv.arr_n)) return false;
             if (kv.arr_type == GgufType::STRING) {
+                // every element takes at least its 8-byte length
+                if (kv.arr_n > (r.size - r.pos) / 8) return false;
+                kv.arr_strs.resize((size_t) kv.arr_n);
                 for (uint64_t i = 0; i < kv.arr_n; ++i) {
-                    std::string s;
-                    if (!r.str(s)) return false;
+                    if (!r.str(kv.arr_strs[(size_t) i])) return false;
                 }
                 return true;
             }
             const size_t es = scalar_size(kv.arr_type);
             if (kv.arr_n > (r.size - r.pos) / es) return false;
-            return r.skip(kv.arr_n * es);
+            const size_t bytes = (size_t) kv.arr_n * es;
+            kv.arr_words.resize((bytes + 7) / 8);
+            return r.take(kv.arr_words.data(), bytes);
         }
         case GgufType::F32: { float v; if (!r.get(v)) return false; kv.f = v; return true; }
         case GgufType::F64: return r.get(kv.f);
@@ -267,6 +273,41 @@ GgufType gguf_kv_type(const GgufFile* f, int64_t index) {
 
 bool gguf_has_key(const GgufFile* f, const char* key) { return gguf_find_key(f, key) >= 0; }
 
+GgufType gguf_arr_type(const GgufFile* f, int64_t index) {
+    TRC_CHECK(index >= 0 && index < (int64_t) f->kvs.size(), "gguf_arr_type: index out of range");
+    const GgufKvEntry& kv = f->kvs[(size_t) index];
+    TRC_CHECK(kv.type == GgufType::ARRAY, "gguf_arr_type: key %s is not an array", kv.key.c_str());
+    return kv.arr_type;
+}
+
+int64_t gguf_arr_count(const GgufFile* f, int64_t index) {
+    TRC_CHECK(index >= 0 && index < (int64_t) f->kvs.size(), "gguf_arr_count: index out of range");
+    const GgufKvEntry& kv = f->kvs[(size_t) index];
+    TRC_CHECK(kv.type == GgufType::ARRAY, "gguf_arr_count: key %s is not an array", kv.key.c_str());
+    return (int64_t) kv.arr_n;
+}
+
+uint8_t gguf_get_u8(const GgufFile* f, const char* key) {
+    const GgufKvEntry* kv = typed_kv(f, key, GgufType::U8);
+    return kv ? (uint8_t) kv->u : 0;
+}
+int8_t gguf_get_i8(const GgufFile* f, const char* key) {
+    const GgufKvEntry* kv = typed_kv(f, key, GgufType::I8);
+    return kv ? (int8_t) (uint8_t) kv->u : 0;
+}
+uint16_t gguf_get_u16(const GgufFile* f, const char* key) {
+    const GgufKvEntry* kv = typed_kv(f, key, GgufType::U16);
+    return kv ? (uint16_t) kv->u : 0;
+}
+int16_t gguf_get_i16(const GgufFile* f, const char* key) {
+    const GgufKvEntry* kv = typed_kv(f, key, GgufType::I16);
+    return kv ? (int16_t) (uint16_t) kv->u : 0;
+}
+double gguf_get_f64(const GgufFile* f, const char* key) {
+    const GgufKvEntry* kv = typed_kv(f, key, GgufType::F64);
+    return kv ? kv->f : 0.0;
+}
+
 uint32_t gguf_get_u32(const GgufFile* f, const char* key) {
     const GgufKvEntry* kv = typed_kv(f, key, GgufType::U32);
     return kv ? (uint32_t) kv->u : 0;
@@ -294,6 +335,47 @@ bool gguf_get_bool(const GgufFile* f, const char* key) {
 const char* gguf_get_str(const GgufFile* f, const char* key) {
     const GgufKvEntry* kv = typed_kv(f, key, GgufType::STRING);
     return kv ? kv->str.c_str() : nullptr;
+}
+
+namespace {
+
+// The array under `key` if its elements are of type `elem` (else an error and nullptr).
+const GgufKvEntry* typed_arr(const GgufFile* f, const char* key, GgufType elem) {
+    const GgufKvEntry* kv = typed_kv(f, key, GgufType::ARRAY);
+    if (kv == nullptr) return nullptr;
+    if (kv->arr_type != elem) {
+        log_error("GGUF: array %s holds type %d, not %d", key, (int) kv->arr_type, (int) elem);
+        return nullptr;
+    }
+    return kv;
+}
+
+template <typename T>
+const T* scalar_array(const GgufFile* f, const char* key, GgufType elem, int64_t* n) {
+    const GgufKvEntry* kv = typed_arr(f, key, elem);
+    if (n != nullptr) *n = kv ? (int64_t) kv->arr_n : 0;
+    return kv ? (const T*) kv->arr_words.data() : nullptr;
+}
+
+}  // namespace
+
+const int32_t* gguf_get_arr_i32(const GgufFile* f, const char* key, int64_t* n) {
+    return scalar_array<int32_t>(f, key, GgufType::I32, n);
+}
+const int64_t* gguf_get_arr_i64(const GgufFile* f, const char* key, int64_t* n) {
+    return scalar_array<int64_t>(f, key, GgufType::I64, n);
+}
+const float* gguf_get_arr_f32(const GgufFile* f, const char* key, int64_t* n) {
+    return scalar_array<float>(f, key, GgufType::F32, n);
+}
+const char* gguf_get_arr_str(const GgufFile* f, const char* key, int64_t index) {
+    const GgufKvEntry* kv = typed_arr(f, key, GgufType::STRING);
+    if (kv == nullptr) return nullptr;
+    if (index < 0 || index >= (int64_t) kv->arr_n) {
+        log_error("GGUF: index %lld out of range for %s", (long long) index, key);
+        return nullptr;
+    }
+    return kv->arr_strs[(size_t) index].c_str();
 }
 
 int64_t gguf_tensor_count(const GgufFile* f) { return (int64_t) f->infos.size(); }
@@ -360,6 +442,73 @@ float half_to_float(uint16_t h) {
     return __builtin_bit_cast(float, bits);
 }
 
+// The legacy block formats decoded on the host, element for element as the
+// reference's dequantize_q* (src/io/trc_gguf.cpp:320-417): (float) q * d, plus m
+// for Q4_1/Q5_1, each * and + rounded on its own (this file is built with
+// -ffp-contract=off). Used by gguf_tensor_to_f32 when no HIP device is there.
+float fp16_field(const uint8_t* p) {
+    uint16_t h;
+    std::memcpy(&h, p, 2);
+    return half_to_float(h);
+}
+
+void dequant_blocks_host(Type type, const uint8_t* src, int64_t n_blocks, float* out) {
+    const size_t bs = type_size(type);
+    for (int64_t i = 0; i < n_blocks; ++i) {
+        const uint8_t* b = src + (size_t) i * bs;
+        float* y = out + i * 32;
+        switch (type) {
+            case TYPE_Q4_0: {  // {d; qs[16]}
+                const float d = fp16_field(b);
+                for (int j = 0; j < 16; ++j) {
+                    y[j] = (float) ((b[2 + j] & 0x0F) - 8) * d;
+                    y[j + 16] = (float) ((b[2 + j] >> 4) - 8) * d;
+                }
+                break;
+            }
+            case TYPE_Q4_1: {  // {d; m; qs[16]}
+                const float d = fp16_field(b), m = fp16_field(b + 2);
+                for (int j = 0; j < 16; ++j) {
+                    y[j] = (float) (b[4 + j] & 0x0F) * d + m;
+                    y[j + 16] = (float) (b[4 + j] >> 4) * d + m;
+                }
+                break;
+            }
+            case TYPE_Q5_0: {  // {d; qh (LE u32); qs[16]}: bit j and j + 16 of qh are the fifth bits
+                const float d = fp16_field(b);
+                uint32_t qh;
+                std::memcpy(&qh, b + 2, 4);
+                for (int j = 0; j < 16; ++j) {
+                    const int lo = (b[6 + j] & 0x0F) | (int) (((qh >> j) & 1u) << 4);
+                    const int hi = (b[6 + j] >> 4) | (int) (((qh >> (j + 16)) & 1u) << 4);
+                    y[j] = (float) (lo - 16) * d;
+                    y[j + 16] = (float) (hi - 16) * d;
+                }
+                break;
+            }
+            case TYPE_Q5_1: {  // {d; m; qh; qs[16]}
+                const float d = fp16_field(b), m = fp16_field(b + 2);
+                uint32_t qh;
+                std::memcpy(&qh, b + 4, 4);
+                for (int j = 0; j < 16; ++j) {
+                    const int lo = (b[8 + j] & 0x0F) | (int) (((qh >> j) & 1u) << 4);
+                    const int hi = (b[8 + j] >> 4) | (int) (((qh >> (j + 16)) & 1u) << 4);
+                    y[j] = (float) lo * d + m;
+                    y[j + 16] = (float) hi * d + m;
+                }
+                break;
+            }
+            case TYPE_Q8_0: {  // {d; qs[32] int8}
+                const float d = fp16_field(b);
+                for (int j = 0; j < 32; ++j) y[j] = (float) (int8_t) b[2 + j] * d;
+                break;
+            }
+            default:
+                break;
+        }
+    }
+}
+
 }  // namespace
 
 bool gguf_tensor_to_f32(const GgufFile* f, const char* name, float* out, int64_t n_elems) {
@@ -384,10 +533,8 @@ bool gguf_tensor_to_f32(const GgufFile* f, const char* name, float* out, int64_t
         case TYPE_I32: convert<int32_t>(src, out, n, [](int32_t v) { return (float) v; }); return true;
         case TYPE_I64: convert<int64_t>(src, out, n, [](int64_t v) { return (float) v; }); return true;
         case TYPE_Q4_0: case TYPE_Q4_1: case TYPE_Q5_0: case TYPE_Q5_1: case TYPE_Q8_0:
-            if (!hip_dequant_host(info->type, src, n / 32, out)) {
-                log_error("GGUF: dequantizing %s needs a HIP device", name);
-                return false;
-            }
+            // on the GPU when one is there (the same bits), else on the host
+            if (!hip_dequant_host(info->type, src, n / 32, out)) dequant_blocks_host(info->type, src, n / 32, out);
             return true;
         default:
             log_error("GGUF: type %s of %s cannot be converted", type_name(info->type), name);

@@ -5,10 +5,7 @@
 
 namespace traincpp {
 
-// If dst lives in a HIP buffer: uploads n_blocks raw blocks of `type` and
-// dequantizes them on the GPU straight into dst (contiguous F32). Returns false
-// when dst is not in a HIP buffer (nothing done); aborts on a HIP error.
-bool hip_dequant_into(Tensor* dst, Type type, const void* host_blocks, int64_t n_blocks);
+// hip_dequant_into (declared in traincpp/trc_hip.h) serves gguf_load_tensor.
 
 // Dequantizes host blocks into host floats through the GPU (device 0).
 // Returns false if no HIP device is available.
