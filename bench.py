@@ -16,12 +16,15 @@ The same run also measures, each against its roofline (`extra`):
 
 Timing: steps are enqueued on one stream and captured into a HIP graph (host
 launch overhead stays out of the timed region); HIP events on that stream
-bracket the K timed replays. Inputs rotate over buffer sets totalling more
+bracket each timed replay of the K launches, and the headline is the median
+over --replays replays (the spread is reported beside it). Inputs rotate over buffer sets totalling more
 than 512 MB so the 256 MB Infinity Cache cannot hold them between steps.
 
 cpu_baseline: the reference CPU path (dequantize the whole weight, then the
 serial mul_mat loop) restated in oracle/ and run single-threaded on this
-host's cores for the headline workload.
+host's cores for the headline workload; extra.cpu_baseline_all_cores runs it
+on every core this process may use (sched_getaffinity), and extra.host names
+the CPU model.
 """
 from __future__ import annotations
 
@@ -93,15 +96,19 @@ class Hip:
 
 class Timer:
     """Times `steps` calls of fn(i) enqueued on one stream, as a HIP graph replay
-    when capture works (falls back to plain stream launches)."""
+    when capture works (falls back to plain stream launches). `replays` timed
+    replays of the same graph; run() returns their median ms per step and keeps
+    every replay's figure in `last_replays`."""
 
-    def __init__(self, hip: Hip, use_graph: bool = True):
+    def __init__(self, hip: Hip, use_graph: bool = True, replays: int = 1):
         self.hip = hip
         self.stream = hip.stream()
         self.e0, self.e1 = hip.event(), hip.event()
         self.use_graph = use_graph
+        self.replays = replays
+        self.last_replays: list[float] = []
 
-    def run(self, fn, steps: int, warmup: int) -> tuple[float, str]:
+    def run(self, fn, steps: int, warmup: int, replays: int | None = None) -> tuple[float, str]:
         hip, rt, s = self.hip, self.hip.rt, self.stream
         for i in range(warmup):
             fn(i, s)
@@ -129,20 +136,23 @@ class Timer:
                 mode = "graph"
             except RuntimeError:
                 exec_ = None
-        hip.ok(rt.hipDeviceSynchronize(), "sync")
-        hip.ok(rt.hipEventRecord(self.e0, s), "record")
-        if exec_ is not None:
-            hip.ok(rt.hipGraphLaunch(exec_, s), "hipGraphLaunch")
-        else:
-            for i in range(steps):
-                fn(warmup + i, s)
-        hip.ok(rt.hipEventRecord(self.e1, s), "record")
-        hip.ok(rt.hipEventSynchronize(self.e1), "sync")
-        hip.ok(rt.hipDeviceSynchronize(), "sync")
-        ms = hip.elapsed_ms(self.e0, self.e1)
+        per_step = []
+        for _ in range(replays or self.replays):
+            hip.ok(rt.hipDeviceSynchronize(), "sync")
+            hip.ok(rt.hipEventRecord(self.e0, s), "record")
+            if exec_ is not None:
+                hip.ok(rt.hipGraphLaunch(exec_, s), "hipGraphLaunch")
+            else:
+                for i in range(steps):
+                    fn(warmup + i, s)
+            hip.ok(rt.hipEventRecord(self.e1, s), "record")
+            hip.ok(rt.hipEventSynchronize(self.e1), "sync")
+            hip.ok(rt.hipDeviceSynchronize(), "sync")
+            per_step.append(hip.elapsed_ms(self.e0, self.e1) / steps)
         if exec_ is not None:
             rt.hipGraphExecDestroy(exec_)
-        return ms / steps, mode
+        self.last_replays = per_step
+        return float(np.median(per_step)), mode
 
 
 # ---------------------------------------------------------------- workloads
@@ -166,12 +176,14 @@ def qmatvec_case(H, synth, timer, t, K, M, N, steps, warmup, cfg=2):
         H.qmatvec(t, ws[j].ptr, K, M, nb1_w, xs[j].ptr, N, K * 4, ys[j].ptr, M * 4, s)
 
     ms, mode = timer.run(step, steps, warmup)
+    reps = list(timer.last_replays)
     for b in ws + xs + ys:
         b.free()
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     flops = 2.0 * K * M * N
     return {"ms": ms, "bytes": alg_bytes, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS,
-            "TFLOP/s": flops / (ms * 1e-3) / 1e12, "sets": sets, "timing": mode}, blk, x
+            "TFLOP/s": flops / (ms * 1e-3) / 1e12, "sets": sets, "timing": mode,
+            "replays_us": [round(r * 1e3, 3) for r in reps]}, blk, x
 
 
 def dequant_case(H, synth, timer, t, n_blocks, steps, warmup):
@@ -286,6 +298,41 @@ def cpu_baseline(blk: np.ndarray, x: np.ndarray, K: int, M: int, budget_s: float
                       f"{threads} thread{'s' if threads > 1 else ''}"}
 
 
+def cpu_host_info() -> dict:
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "cores_available": len(os.sched_getaffinity(0)), "os_cpu_count": os.cpu_count()}
+
+
+def gguf_load_cfg0_reference_route(H, synth, threads: int, reps: int = 5):
+    """The reference's gguf_load_tensor route for configuration 0 on this host:
+    dequantize the Q8_0 blocks on the host (its serial loops, restated in
+    oracle/, 1 thread) into an F32 vector, then upload the 64 MiB F32 weight."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+    lib = O.oracle()
+    K = M = 4096
+    n = K * M // 32
+    raw = synth.block_bytes(synth.quant_blocks(H.TYPE_Q8_0, n, synth.config_seed(0, 8)))
+    w = H.DeviceBuffer(K * M * 4)
+    times = []
+    for r in range(reps + 1):
+        t0 = time.perf_counter()
+        f32 = np.empty(K * M, np.float32)
+        assert lib.orc_dequant(H.TYPE_Q8_0, raw.ctypes.data, n, f32.ctypes.data, threads) == 0
+        w.upload(f32)
+        times.append(time.perf_counter() - t0)
+    w.free()
+    return {"ms": float(np.median(times[1:])) * 1e3, "threads": threads,
+            "sample": "Q8_0 4096x4096 blocks in memory -> host dequant (oracle/oracle.cpp) -> 64 MiB H2D"}
+
+
 def cpu_other_paths(synth, budget_s: float, threads: int):
     """The reference CPU path of the other two hot paths on this host, one thread
     and `threads` threads (same bits): H1 = gguf_tensor_to_f32's quant branch on
@@ -345,6 +392,53 @@ def read_traffic():
         return None
 
 
+def write_gguf_q8_0(path: str, raw: np.ndarray, K: int, M: int) -> int:
+    """A one-tensor GGUF v3 file (tensor "w", Q8_0 [K, M], 32-byte alignment); returns
+    the byte offset of the tensor data."""
+    import struct
+    head = bytearray(b"GGUF") + struct.pack("<IQQ", 3, 1, 1)
+    key, val = b"general.architecture", b"linear"
+    head += struct.pack("<Q", len(key)) + key + struct.pack("<iQ", 8, len(val)) + val
+    head += struct.pack("<Q", 1) + b"w" + struct.pack("<IqqIQ", 2, K, M, 8, 0)
+    head += bytes(-len(head) % 32)
+    with open(path, "wb") as f:
+        f.write(head)
+        f.write(raw.tobytes())
+        f.write(bytes(-raw.nbytes % 32))
+    return len(head)
+
+
+def gguf_load_cfg0(H, synth, reps: int = 7):
+    """Configuration 0's warm start through the C ABI as hip_gguf_load_tensor does
+    it: the Q8_0 blocks of a GGUF file (page-cache resident) mapped with mmap,
+    uploaded raw (17.8 MB) and dequantized in HBM into the F32 weight (64 MiB).
+    Median wall time over `reps` loads after one untimed load."""
+    import tempfile
+    K = M = 4096
+    n = K * M // 32
+    raw = synth.block_bytes(synth.quant_blocks(H.TYPE_Q8_0, n, synth.config_seed(0, 8)))
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "cfg0.gguf")
+        off = write_gguf_q8_0(path, raw, K, M)
+        blocks = H.DeviceBuffer(raw.nbytes)
+        w = H.DeviceBuffer(K * M * 4)
+        times = []
+        for r in range(reps + 1):
+            t0 = time.perf_counter()
+            mm = np.memmap(path, dtype=np.uint8, mode="r", offset=off, shape=(raw.nbytes,))
+            blocks.upload(mm)
+            H.dequant(H.TYPE_Q8_0, blocks.ptr, n, w.ptr)
+            H.sync()
+            times.append(time.perf_counter() - t0)
+            del mm
+        blocks.free()
+        w.free()
+    t = float(np.median(times[1:]))
+    return {"ms": t * 1e3, "ms_replays": [round(v * 1e3, 3) for v in times[1:]],
+            "bytes_uploaded": int(raw.nbytes), "f32_bytes_in_hbm": K * M * 4,
+            "file": "page-cache resident GGUF v3, mmap + pageable H2D + trc_hip_dequant"}
+
+
 def copy_calibration(H, timer, steps, warmup):
     """A plain device copy of a known size (256 MiB read + 256 MiB written) through
     trc_hip_cpy: the reference point that scales the HBM traffic counters."""
@@ -366,6 +460,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--replays", type=int, default=7,
+                    help="timed replays of the headline's graph of --steps launches; the median is reported")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -386,7 +482,7 @@ def main():
     from traincpp_amd import synth
     props = H.init(0)
     hip = Hip()
-    timer = Timer(hip, use_graph=not args.no_graph)
+    timer = Timer(hip, use_graph=not args.no_graph, replays=3)
     K, M = 4096, 14336
     if args.calibrate_copy:
         print(json.dumps({"calibration": "copy", **copy_calibration(H, timer, args.steps, args.warmup)}), flush=True)
@@ -410,8 +506,11 @@ def main():
         return
 
     t_wall = time.perf_counter()
+    timer.replays = args.replays
     head, blk, x = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 1, args.steps, args.warmup)
+    timer.replays = 3
     wall = time.perf_counter() - t_wall
+    reps = head["replays_us"]
     traffic = read_traffic()
     roofline = {"bound": "hbm", "achieved": head["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": head["GB/s"] / HBM_PEAK_GBS, "traffic": traffic,
@@ -441,14 +540,19 @@ def main():
             extra["dequant_4096x11008"][name] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
         extra["mul_mat_cfg3_linear_4096x4096x512"] = mul_mat_config3(H, synth, timer, max(10, s // 4), 3)
         extra["mul_mat_cfg4_batched_permuted"] = mul_mat_config4(H, synth, timer, max(10, s // 4), 3)
+        extra["gguf_load_cfg0_hip_route"] = gguf_load_cfg0(H, synth)
 
+    host = cpu_host_info()
     cpu = cpu_baseline(blk, x, K, M, args.cpu_budget)
+    cpu["cpu_model"] = host["cpu_model"]
     extra["cpu_vs_gpu_speedup"] = head["GB/s"] / cpu["value"]
+    extra["host"] = host
     if not args.headline_only:
-        # the same path on the host's cores (a GPU box's share is 16), outputs split over threads
-        nt = max(1, min(16, os.cpu_count() or 1))
+        # the same path on every core this process may run on, outputs split over threads
+        nt = max(1, host["cores_available"])
         extra["cpu_baseline_all_cores"] = cpu_baseline(blk, x, K, M, args.cpu_budget / 4, nt)
         extra["cpu_other_paths"] = cpu_other_paths(synth, args.cpu_budget / 5, nt)
+        extra["cpu_other_paths"]["gguf_load_cfg0_reference_route"] = gguf_load_cfg0_reference_route(H, synth, 1)
 
     line = {
         "metric": METRIC,
@@ -465,6 +569,11 @@ def main():
         "data": "synthetic (seeded splitmix64: Q4_0 blocks with d~U[2e-4,1e-3] fp16, nibbles U{0..15}; x~N(0,1))",
         "config": {"workload": "cfg2 decode: fused Q4_0 dequant-matvec, W[K=4096,M=14336] x F32 x[4096,1]",
                    "K": K, "M": M, "N": 1, "rotating_sets": head["sets"], "timing": head["timing"],
+                   "x_arithmetic": "x in 24-bit block fixed point (a power-of-two scale per 32-element block), "
+                                   "exact int32 digit dot products against the quants, f32 block scaling and "
+                                   "accumulation",
+                   "headline_stat": f"median of {len(reps)} graph replays of {args.steps} launches each",
+                   "replays_us": reps, "spread_us": round(max(reps) - min(reps), 3),
                    "wall_s_headline": round(wall, 3)},
         "roofline": roofline,
         "cpu_baseline": cpu,
