@@ -24,6 +24,8 @@
 // kernel in qmm.hip.
 #include "common.h"
 
+#include <type_traits>
+
 namespace trc_hip {
 namespace {
 
@@ -858,16 +860,33 @@ __device__ __forceinline__ void qd_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds,
 // s_waitcnt immediate with vmcnt = v (bits 3:0 and 15:14), the others at their maximum.
 constexpr int qd_vmcnt(int v) { return (v & 0xF) | ((v >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
-// Wait until at most k rows of NI copies each are outstanding. vmcnt also counts
-// the stores issued after a row's copies, so this waits at least as long as needed.
+// Wait until at most k rows of NI copies each, and the st store instructions
+// issued after the row being waited for, are outstanding. vmcnt counts loads and
+// stores together and retires them in issue order, so the count must include
+// every store issued after the row's copies, and no more. Callers pass
+// compile-time constants, so the switch folds to one wait.
 template <int NI>
-__device__ __forceinline__ void qd_wait_rows(int k) {
-    static_assert(2 * NI < 64, "vmcnt is 6 bits");
-    switch (k) {
-        case 0: __builtin_amdgcn_s_waitcnt(qd_vmcnt(0)); break;
-        case 1: __builtin_amdgcn_s_waitcnt(qd_vmcnt(NI)); break;
-        default: __builtin_amdgcn_s_waitcnt(qd_vmcnt(2 * NI)); break;
+__device__ __forceinline__ void qd_wait_rows(int k, int st = 0) {
+    static_assert(2 * NI + 8 < 64, "vmcnt is 6 bits");
+    switch (k * NI + st) {
+#define QD_WAIT_CASE(n) case n: __builtin_amdgcn_s_waitcnt(qd_vmcnt(n)); break;
+        QD_WAIT_CASE(0) QD_WAIT_CASE(1) QD_WAIT_CASE(2) QD_WAIT_CASE(3) QD_WAIT_CASE(4) QD_WAIT_CASE(5)
+        QD_WAIT_CASE(6) QD_WAIT_CASE(7) QD_WAIT_CASE(8) QD_WAIT_CASE(9) QD_WAIT_CASE(10) QD_WAIT_CASE(11)
+        QD_WAIT_CASE(12) QD_WAIT_CASE(13) QD_WAIT_CASE(14) QD_WAIT_CASE(15) QD_WAIT_CASE(16) QD_WAIT_CASE(17)
+        QD_WAIT_CASE(18)
+#undef QD_WAIT_CASE
+        default: __builtin_amdgcn_s_waitcnt(qd_vmcnt(0)); break;  // not reached: waits for everything
     }
+}
+
+// Workgroup b's place in row order, so that consecutive row slots belong to the
+// workgroups of one XCD. The dispatcher deals workgroups to the 8 XCDs round
+// robin (b mod 8), and each XCD has its own L2: with this order the rows whose
+// results share an output cache line are computed, and their stores merged, in
+// one L2. A bijection on [0, nb) for any nb.
+__device__ __forceinline__ int64_t qd_xcd_slot(int64_t b, int64_t nb) {
+    const int64_t x = b & 7, per = nb >> 3, extra = nb & 7;
+    return x * per + (x < extra ? x : extra) + (b >> 3);
 }
 
 // The PW dwords of a pair at LDS byte address a, read and waited for in one asm
@@ -930,17 +949,26 @@ __device__ __forceinline__ void qd_lds_words<17>(uint32_t a, uint32_t (&w)[17]) 
 // would also wait for every LDS copy in flight, which drains the weight stream.
 __device__ __forceinline__ void qd_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// NC columns of x (1 or 2) share one pass over W: each row's quant words are
+// NC columns of x (1 to 4) share one pass over W: each row's quant words are
 // decoded once and met by every column's digit planes (48 registers per column).
 // DMA: weight rows through LDS (needs 16-byte aligned rows and nblk % 8 == 0);
 // otherwise each lane loads its pair into registers.
-template <int TYPE, int RPW, int NC, bool DMA, int PF_ROWS>
+// PSTORE (in the last chunk): 0 = the wave stores all its rows with one
+// instruction per column after its last load; 1 = each row is stored as soon as
+// it is reduced, inside the weight stream (lane r stores row r; the wait counts
+// of the rows behind it include these stores); 2 = the rows done when the wave
+// issues its last copies are stored right then, in one instruction per column
+// (no wait for a copy counts them), and the last PF rows at the end.
+// ONE: K is one chunk (nblk <= QD_CH), compiled without the chunk loop.
+template <int TYPE, int RPW, int NC, bool DMA, int PF_ROWS, int PSTORE, bool ONE = false>
 __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __restrict__ W, int64_t nblk, int64_t M,
                                                      int64_t nb1_w, const float* __restrict__ x, int64_t ldx,
                                                      float* __restrict__ y, int64_t ldy) {
     constexpr int BYTES = block_bytes(TYPE);
     constexpr int PW = QdFmt<TYPE>::PAIR_WORDS;
-    constexpr int PF = PF_ROWS < RPW ? PF_ROWS : RPW;
+    // two-row waves with the early store keep one row in flight, so that row 0 is
+    // stored while row 1 streams (M = 4096: 4 % faster than both rows at once)
+    constexpr int PF = PSTORE == 2 && RPW == 2 ? 1 : PF_ROWS < RPW ? PF_ROWS : RPW;
     static_assert(RPW <= 64, "each of a wave's rows is stored by one lane");
     constexpr int SEG = QD_CH * BYTES;        // bytes of a row's full chunk
     constexpr int NI = (SEG + 1023) / 1024;   // 16-byte copies per lane and row
@@ -952,7 +980,7 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
 
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t wave_id = (int64_t) blockIdx.x * QD_WAVES + wv;
+    const int64_t wave_id = qd_xcd_slot(blockIdx.x, gridDim.x) * QD_WAVES + wv;
     // Rows are strided over the waves (row = wave + r * n_waves), so the loads
     // in flight at any time sweep W in address order rather than starting in
     // every wave's own region.
@@ -978,7 +1006,11 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
 
     const int64_t nchunks = (nblk + QD_CH - 1) / QD_CH;
     uint32_t w[DMA ? 1 : RPW][PW];
-    for (int64_t c = 0; c < nchunks; ++c) {
+    // One chunk of K. The last chunk is its own instance (LAST) so that its row
+    // stores, and the wait counts that include them, are compile-time constants
+    // (under a runtime condition the compiler added a conservative wait after
+    // the merge).
+    auto chunk = [&](int64_t c, auto last_tag) {
         const int64_t cb = nblk - c * QD_CH < QD_CH ? nblk - c * QD_CH : QD_CH;
         const bool mine = 2 * lane < cb;  // this lane owns a pair of this chunk (cb is even)
         const int pl = mine ? lane : (int) (cb / 2) - 1;
@@ -998,10 +1030,17 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
                 for (int i = 0; i < PW; ++i) w[r][i] = p32[i];
             }
         };
+        // store instructions issued after row r's copies: one per column for
+        // each of the (at most PF) rows before it, in the last chunk only
+        constexpr bool LAST = decltype(last_tag)::value;
         // this lane's pair of row r, in registers
         auto pair_words = [&](int r) -> const uint32_t* {
             if constexpr (DMA) {
-                qd_wait_rows<NI>(RPW - 1 - r < PF ? RPW - 1 - r : PF);
+                constexpr int MID = RPW - 1 - PF;  // PSTORE 2: the row after which the early rows are stored
+                const int st = !LAST || PSTORE == 0 ? 0
+                               : PSTORE == 1        ? NC * (r < PF ? r : PF)
+                                                    : (MID >= 0 && r > MID ? NC : 0);
+                qd_wait_rows<NI>(RPW - 1 - r < PF ? RPW - 1 - r : PF, st);
                 const uint32_t a = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) uint8_t*) &wring[wv][r % SLOTS][0] +
                                    (uint32_t) pl * (PW * 4);
                 qd_lds_words<PW>(a, w[0]);
@@ -1076,16 +1115,39 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_dot(const uint8_t* __
                 const float s63 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 63));
                 out[n] = lane == r ? (c == 0 ? s63 : out[n] + s63) : out[n];
             }
+            if constexpr (PSTORE == 1 && LAST) {
+                const int64_t row = wave_id + r * n_waves;
+#pragma unroll
+                for (int n = 0; n < NC; ++n)
+                    if (lane == r && row < M) y[n * ldy + row] = out[n];
+            }
+            if constexpr (PSTORE == 2 && LAST) {
+                if (r == RPW - 1 - PF) {
+                    const int64_t row = wave_id + (int64_t) lane * n_waves;
+#pragma unroll
+                    for (int n = 0; n < NC; ++n)
+                        if (lane <= r && row < M) y[n * ldy + row] = out[n];
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    if constexpr (ONE) {
+        chunk(0, std::true_type{});
+    } else if constexpr (PSTORE != 0) {
+        for (int64_t c = 0; c + 1 < nchunks; ++c) chunk(c, std::false_type{});
+        chunk(nchunks - 1, std::true_type{});
+    } else {
+        for (int64_t c = 0; c < nchunks; ++c) chunk(c, std::false_type{});
     }
-    // One store per column for all of the wave's rows, after the last load: a
-    // store inside the stream holds up the in-order wait for the rows behind it
-    // (measured: 0.2 us per Q4_0 call, 0.6 us per Q8_0 call at K=4096, M=14336).
-    const int64_t row = wave_id + (int64_t) lane * n_waves;
+    if constexpr (PSTORE != 1) {
+        // one store per column for the wave's rows not stored yet, after the last load
+        constexpr int FIRST = PSTORE == 2 ? (RPW - PF > 0 ? RPW - PF : 0) : 0;
+        const int64_t row = wave_id + (int64_t) lane * n_waves;
 #pragma unroll
-    for (int n = 0; n < NC; ++n)
-        if (lane < RPW && row < M) y[n * ldy + row] = out[n];
+        for (int n = 0; n < NC; ++n)
+            if (lane >= FIRST && lane < RPW && row < M) y[n * ldy + row] = out[n];
+    }
 }
 
 // One or two columns with K in 2..CS chunks of QD_CH blocks (the weights
@@ -1239,6 +1301,45 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_qmatvec_kslots(const uint8_t*
     }
 }
 
+// Where k_qmatvec_dot stores its rows (PSTORE), as measured against one store
+// per column after the last load (configuration 2, M = 14336, graph replays):
+// with K in one chunk through LDS, storing the rows done at the last copy issue
+// right then (2) is 2-3.4 % faster for one column of every format (per-row
+// stores: Q5_0 1 % slower) and within 0.5 % for two to four columns; for Q8_0
+// over four chunks (K = 14336) and on the register path per-row stores (1) are
+// 2 % faster, and Q4_0 on the register path 3 % slower.
+constexpr int qd_pstore(int type, int nc, bool dma, bool one) {
+    if (dma && one) return 2;
+    return type == TRC_HIP_TYPE_Q8_0 && nc <= 3 ? 1 : 0;
+}
+
+template <int TYPE, int RPW, int NC, bool ONE>
+int launch_dot_one(const uint8_t* w, int64_t nblk, int64_t M, size_t nb1_w, const float* x, int64_t ldx, float* y,
+                   int64_t ldy, bool dma, int64_t grid, hipStream_t s) {
+    const dim3 g((unsigned) grid), b(QD_WAVES * 64);
+    // only the largest row count per wave can leave more workgroups than CUs
+    if constexpr (RPW == QD_RMAX) {
+        if (dma && grid > device_cus()) {
+            constexpr int PF = qd_prefetch(TYPE, NC, true, true);
+            hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true, PF, qd_pstore(TYPE, NC, true, ONE), ONE>), g, b, 0, s,
+                               w, nblk, M, (int64_t) nb1_w, x, ldx, y, ldy);
+            return check_launch("qmatvec_dot");
+        }
+    }
+    if (dma) {
+        constexpr int PF = qd_prefetch(TYPE, NC, true, false);
+        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true, PF, qd_pstore(TYPE, NC, true, ONE), ONE>), g, b, 0, s, w,
+                           nblk, M, (int64_t) nb1_w, x, ldx, y, ldy);
+    } else if constexpr (NC <= 2) {
+        constexpr int PF = qd_prefetch(TYPE, NC, false, false);
+        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, false, PF, qd_pstore(TYPE, NC, false, ONE), ONE>), g, b, 0, s,
+                           w, nblk, M, (int64_t) nb1_w, x, ldx, y, ldy);
+    } else {
+        return fail(TRC_HIP_E_INVALID, "qmatvec: %d columns need the LDS path", NC);
+    }
+    return check_launch("qmatvec_dot");
+}
+
 template <int TYPE, int RPW, int NC>
 int launch_dot_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, float* y,
                    size_t nb1_y, hipStream_t s) {
@@ -1246,30 +1347,13 @@ int launch_dot_rpw(const void* wq, int64_t nblk, int64_t M, size_t nb1_w, const 
     const int64_t grid = (waves + QD_WAVES - 1) / QD_WAVES;
     // the LDS copies need 16-byte aligned row chunks (8 blocks are a multiple of 16 bytes)
     const bool dma = nblk % 8 == 0 && (((uintptr_t) wq) & 15u) == 0 && (nb1_w & 15u) == 0;
-    const dim3 g((unsigned) grid), b(QD_WAVES * 64);
     const int64_t ldx = (int64_t) (nb1_x / sizeof(float)), ldy = (int64_t) (nb1_y / sizeof(float));
     const auto* w = (const uint8_t*) wq;
-    // only the largest row count per wave can leave more workgroups than CUs
-    if constexpr (RPW == QD_RMAX) {
-        if (dma && grid > device_cus()) {
-            constexpr int PF = qd_prefetch(TYPE, NC, true, true);
-            hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true, PF>), g, b, 0, s, w, nblk, M, (int64_t) nb1_w, x,
-                               ldx, y, ldy);
-            return check_launch("qmatvec_dot");
-        }
-    }
-    if (dma) {
-        constexpr int PF = qd_prefetch(TYPE, NC, true, false);
-        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true, PF>), g, b, 0, s, w, nblk, M, (int64_t) nb1_w, x, ldx,
-                           y, ldy);
-    } else if constexpr (NC <= 2) {
-        constexpr int PF = qd_prefetch(TYPE, NC, false, false);
-        hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, false, PF>), g, b, 0, s, w, nblk, M, (int64_t) nb1_w, x, ldx,
-                           y, ldy);
-    } else {
-        return fail(TRC_HIP_E_INVALID, "qmatvec: %d columns need the LDS path", NC);
-    }
-    return check_launch("qmatvec_dot");
+    // K in one chunk (every decode shape with K <= 4096) runs an instance
+    // without the chunk loop: 1-5 % faster, measured over the five formats and
+    // one to four columns
+    if (nblk <= QD_CH) return launch_dot_one<TYPE, RPW, NC, true>(w, nblk, M, nb1_w, x, ldx, y, ldy, dma, grid, s);
+    return launch_dot_one<TYPE, RPW, NC, false>(w, nblk, M, nb1_w, x, ldx, y, ldy, dma, grid, s);
 }
 
 template <int TYPE, int NC>
