@@ -467,7 +467,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time a 256 MiB device copy (reference for the traffic counters)")
-    ap.add_argument("--only", choices=["dequant", "mul_mat", "qmm", "qmm_sweep"],
+    ap.add_argument("--only", choices=["dequant", "mul_mat", "qmm", "cfg0", "qmm_sweep"],
                     help="only time one hot path and print its figures (for counter runs): dequant = the five "
                          "formats on configuration 1, mul_mat = configurations 3 and 4, qmm = Q4_0 N=16 on "
                          "configuration 2, qmm_sweep = Q4_0 on configuration 2 for N from 1 to 64")
@@ -497,6 +497,9 @@ def main():
             part["cfg4"] = mul_mat_config4(H, synth, timer, args.steps, args.warmup)
         elif args.only == "qmm":
             part["q4_0 N=16"], _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 16, args.steps, args.warmup)
+        elif args.only == "cfg0":
+            part["q8_0 4096x4096 N=8"], _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q8_0, 4096, 4096, 8, args.steps,
+                                                           args.warmup, cfg=0)
         else:
             for n in (1, 2, 3, 4, 8, 12, 16, 17, 24, 32, 33, 48, 64):
                 r, _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, n, args.steps, args.warmup)
