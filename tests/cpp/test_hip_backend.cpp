@@ -595,6 +595,23 @@ void test_core_cpu(const std::string& dir) {
     Graph* g = graph_new(ctx);
     graph_build_forward_expand(ctx, g, y);
     EXPECT(graph_n_nodes(g) == 3 && graph_node(g, 2) == y && graph_n_leafs(g) == 2);
+    {
+        // a node's sources end at its first null entry, as in the reference's
+        // expansion (src/core/trc_graph.cpp:59-61): src[2] behind a null src[1]
+        // is not visited
+        Graph* g2 = graph_new(ctx);
+        Tensor* n3 = new_tensor_1d(ctx, TYPE_F32, 4);
+        Tensor* s0 = new_tensor_1d(ctx, TYPE_F32, 4);
+        Tensor* s2 = new_tensor_1d(ctx, TYPE_F32, 4);
+        n3->op = OP_ADD;
+        n3->src[0] = s0;
+        n3->src[1] = nullptr;
+        n3->src[2] = s2;
+        n3->nsrc = 3;
+        graph_build_forward_expand(ctx, g2, n3);
+        EXPECT(graph_n_nodes(g2) == 2 && graph_node(g2, 0) == s0 && graph_node(g2, 1) == n3);
+        graph_free(g2);
+    }
     EXPECT(std::string(op_name(OP_MUL_MAT)) == "mul_mat" && std::string(op_name(OP_WEIGHTNORM_SYNC)) == "weightnorm_sync");
     EXPECT(std::string(type_name(TYPE_Q5_1)) == "q5_1" && type_size(TYPE_Q8_0) == 34 && type_blck_size(TYPE_Q4_1) == 32);
     // add / repeat_back / acc nodes (src/ops/trc_ops.cpp:46,458-470; src/core/trc_tensor.cpp:322-361)

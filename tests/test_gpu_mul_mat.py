@@ -152,7 +152,28 @@ def config3_inputs():
     return W, X, dY
 
 
-COLS = [0, 1, 63, 64, 200, 511]
+# sampled dst rows (ne1 indices) at full size: tile edges, both ends and a stride
+COLS = sorted({0, 1, 31, 32, 63, 64, 127, 128, 200, 255, 256, 383, 384, 510, 511, *range(5, 512, 37)})
+
+
+def sums_error(got, av, bv):
+    """Every dst element enters two float64 checksums that the operands fix:
+    sum_j dst[i, j] = sum_k a[k, i] * (sum_j b[k, j]) and
+    sum_i dst[i, j] = sum_k (sum_i a[k, i]) * b[k, j], per plane (a's planes by the
+    ggml modulo broadcast). Returns the larger row-L2-normalised error of the two;
+    a wrong or missing tile anywhere moves one of them far above FP32 rounding."""
+    ne3, ne2 = got.shape[0], got.shape[1]
+    worst = 0.0
+    for i3 in range(ne3):
+        for i2 in range(ne2):
+            a = np.asarray(av[i3 % av.shape[0], i2 % av.shape[1]], dtype=np.float64)  # [M, K]
+            b = np.asarray(bv[i3, i2], dtype=np.float64)                              # [N, K]
+            d = np.asarray(got[i3, i2], dtype=np.float64)                             # [N, M]
+            s_i, r_i = d.sum(axis=0), a @ b.sum(axis=0)
+            s_j, r_j = d.sum(axis=1), b @ a.sum(axis=0)
+            for s, r in ((s_i, r_i), (s_j, r_j)):
+                worst = max(worst, float(np.abs(s - r).max() / max(np.linalg.norm(r), 1e-30)))
+    return worst
 
 
 @pytest.fixture(scope="module")
@@ -178,6 +199,7 @@ def test_config3_full_size(hip, cfg3, product):
     want = sampled_oracle_cols(av, bv, cols)
     assert O.row_l2_error(got[:, :, cols, :], want) <= TOL
     assert np.isfinite(got).all()
+    assert sums_error(got, av, bv) <= 1e-5
     da.free()
     db.free()
 
@@ -193,9 +215,10 @@ def test_config4_broadcast_permuted(hip):
     ne, nb = O.view_meta(bv)
     assert ne == [128, 512, 32, 4] and nb == [4, 16384, 512, 8388608]
     got = gpu_mul_mat(da, da.base, db, bv)
-    cols = [0, 7, 300, 511]
+    cols = [0, 7, 31, 32, 255, 256, 300, 480, 511]
     want = sampled_oracle_cols(da.base, bv, cols)
     assert O.row_l2_error(got[:, :, cols, :], want) <= TOL
+    assert sums_error(got, da.base, bv) <= 1e-5
     da.free()
     db.free()
 

@@ -30,9 +30,10 @@ void graph_build_forward_expand(Context* ctx, Graph* graph, Tensor* tensor) {
     std::vector<std::pair<Tensor*, int>> stack{{tensor, 0}};
     while (!stack.empty()) {
         auto& [node, next] = stack.back();
-        if (next < node->nsrc) {
+        // a node's sources end at its first null entry (src/core/trc_graph.cpp:59-61)
+        if (next < node->nsrc && node->src[next] != nullptr) {
             Tensor* s = node->src[next++];
-            if (s != nullptr && !graph->visited.count(s)) stack.push_back({s, 0});
+            if (!graph->visited.count(s)) stack.push_back({s, 0});
             continue;
         }
         Tensor* done = node;
