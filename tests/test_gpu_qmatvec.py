@@ -58,16 +58,20 @@ def test_config2_decode_shapes(hip, name, N):
 @pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("N", [1, 2, 3, 4])
 @pytest.mark.parametrize("K,M,w_off", [(32 * 130, 3001, 0), (32 * 264, 999, 4), (32 * 264, 999, 0), (512, 20000, 0),
-                                       (32 * 200, 777, 0), (16384, 300, 0)])
+                                       (32 * 200, 777, 0), (16384, 300, 0), (32 * 126, 1000, 0), (4096, 3001, 0),
+                                       (4096, 14000, 0)])
 def test_dot_kernel_weight_paths(hip, name, N, K, M, w_off):
     """The one- to four-column kernels' ways of reading W (three and four
     columns only through LDS, four only within one chunk and not for Q4_0; the
     other cases take the matrix-core kernel): into registers (130
-    blocks per row, not a multiple of 8; or W 4 bytes off a 16-byte boundary),
-    through LDS over two full chunks of 128 blocks and a short one (264 blocks;
-    one column: one chunk per wave, a fourth slot idle), two chunks (200 blocks)
-    and four full ones (512 blocks), and through LDS with more workgroups than
-    CUs (20000 rows of 8 per wave)."""
+    blocks per row, not a multiple of 8; or W 4 bytes off a 16-byte boundary;
+    or 126 blocks, K in one chunk), through LDS over two full chunks of 128
+    blocks and a short one (264 blocks; one column: one chunk per wave, a fourth
+    slot idle), two chunks (200 blocks) and four full ones (512 blocks), through
+    LDS with more workgroups than CUs (20000 rows of 8 per wave), and with K in
+    one chunk (the instance without the chunk loop, where rows are stored when
+    a wave issues its last copies): two rows per wave with one in flight (3001
+    rows) and seven rows per wave with rows past M (14000)."""
     t = TYPES[name]
     announce(f"qmatvec dot paths {name} N={N} K={K} M={M} w_off={w_off}")
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 1000 + K + M))
