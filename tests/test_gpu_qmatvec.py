@@ -131,11 +131,13 @@ def test_argument_errors(hip):
 
 # The fp16 matrix-core kernel (qmm.hip) takes 2 <= N <= 16 with a multiple of
 # 8 blocks per row (K % 256 == 0), in chunks of 16 blocks; the cases below pin
-# its layouts, grid shapes, partial last chunks and numerics. Other block
-# counts above exercise the fallback kernels.
+# its layouts, grid shapes, partial last chunks and numerics. Up to 8 columns it
+# packs each column's hi and lo x planes into one 16-column tile, above that it
+# gives each plane its own MFMA. Other block counts above exercise the fallback
+# kernels.
 
 @pytest.mark.parametrize("name", list(TYPES))
-@pytest.mark.parametrize("N", [2, 3, 7, 16])
+@pytest.mark.parametrize("N", [2, 3, 5, 7, 8, 16])
 def test_mfma_path_all_formats(hip, name, N):
     t = TYPES[name]
     K, M = 32 * 40, 301  # 20 pairs: two full chunks and a half one; M not a tile multiple
@@ -149,11 +151,13 @@ def test_mfma_path_all_formats(hip, name, N):
 
 @pytest.mark.parametrize("name", ["q4_0", "q5_1", "q8_0"])
 @pytest.mark.parametrize("M", [1, 5, 16, 250, 3000, 20000])
-def test_mfma_grid_shapes(hip, name, M):
-    """Rows per workgroup from 8 to 64 (1 to 4 tiles), masked tail rows."""
+@pytest.mark.parametrize("N", [8, 16])
+def test_mfma_grid_shapes(hip, name, M, N):
+    """Rows per workgroup from 8 to 64 (1 to 4 tiles), masked tail rows, K in
+    one part or two (up to 24 rows per CU), packed (N = 8) or not."""
     t = TYPES[name]
-    K, N = 256 * 3, 16
-    announce(f"qmm grid {name} K={K} M={M}")
+    K = 256 * 3
+    announce(f"qmm grid {name} K={K} M={M} N={N}")
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 3 + M))
     X = synth.normal(17 + M, K * N).reshape(1, 1, N, K)
     got = gpu_qmatvec(t, raw, K, M, X, x_pad=8, y_pad=5)
@@ -162,18 +166,23 @@ def test_mfma_grid_shapes(hip, name, M):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
-def test_mfma_dynamic_range(hip, name):
+@pytest.mark.parametrize("N", [8, 9])
+def test_mfma_dynamic_range(hip, name, N):
     """Columns of very different magnitude, blocks of very different magnitude
-    inside one column, and denormal x: the scale is per block and column."""
+    inside one column, and denormal x: the scale is per block and column, with
+    hi and lo packed into one tile (N = 8) or not (N = 9)."""
     t = TYPES[name]
-    K, M, N = 32 * 16, 96, 9
-    announce(f"qmm range {name}")
+    K, M = 32 * 16, 96
+    announce(f"qmm range {name} N={N}")
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 77 + t))
     X = synth.normal(5, K * N).reshape(1, 1, N, K).astype(np.float32)
-    col_scale = np.array([1e-30, 1e-6, 1e-3, 1.0, 1e3, 1e6, 1e20, 3e25, 1.0], np.float32)
+    scales = [1e-30, 1e-6, 1e-3, 1.0, 1e3, 1e6, 1e20, 3e25, 1.0]
+    if N == 8:
+        del scales[6]
+    col_scale = np.array(scales, np.float32)
     X *= col_scale[None, None, :, None]
-    X[0, 0, 8, 64:96] *= np.float32(1e12)  # one loud block in an otherwise unit column
-    X[0, 0, 8, 96:128] *= np.float32(1e-12)  # and a quiet one
+    X[0, 0, N - 1, 64:96] *= np.float32(1e12)  # one loud block in an otherwise unit column
+    X[0, 0, N - 1, 96:128] *= np.float32(1e-12)  # and a quiet one
     X[0, 0, 3, 0:32] = np.float32(1e-40)  # a block of denormals next to normal blocks
     got = gpu_qmatvec(t, raw, K, M, X)
     want = oracle_qmatvec(t, raw, K, M, X)
@@ -182,14 +191,15 @@ def test_mfma_dynamic_range(hip, name):
 
 
 @pytest.mark.parametrize("name", ["q4_0", "q5_1", "q8_0"])
-@pytest.mark.parametrize("N", [1, 2, 4])
+@pytest.mark.parametrize("N", [1, 2, 4, 6, 12])
 @pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
 @pytest.mark.parametrize("K", [256, 32 * 296])
 def test_nonfinite_x(hip, name, N, bad, K):
     """A non-finite x element makes its column non-finite, as in the reference
     (the fixed-point kernels return NaN there); the other columns are unaffected.
     Covers the integer-dot (N = 1, 2), one-chunk-per-wave (N = 1, 296 blocks:
-    the element sits in the third chunk) and fp16 MFMA (N = 4) kernels."""
+    the element sits in the third chunk) and fp16 MFMA (N = 4 for Q4_0, packed
+    N = 6, unpacked N = 12) kernels."""
     t = TYPES[name]
     M = 40
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 8))

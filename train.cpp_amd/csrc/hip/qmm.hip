@@ -16,7 +16,10 @@
 // significant bits. Both planes go through the MFMA into one fp32 accumulator
 // (every product of an 11-bit and a 9-bit integer is exact), so a block needs
 // one fused multiply-add by d per output, and each pair's sum is scaled back by
-// its chunk's 2^-s once. An element keeps ~22 bits of its own magnitude down to
+// its chunk's 2^-s once. Up to 8 columns, hi and lo share one 16-column tile
+// instead (packed: rows 0..7 of the A operand hold hi of columns 0..7, rows
+// 8..15 their lo), so each block takes one MFMA and one x load; rows j and j + 8
+// of the result are added once at the end. An element keeps ~22 bits of its own magnitude down to
 // 2^17 below its chunk's largest |x|; below that its absolute error stays under
 // 2^-39 of that largest |x|, so outputs carry FP32-level error. A chunk holding
 // Inf or NaN makes its column come out NaN. (One scale per column would save
@@ -96,6 +99,10 @@ constexpr bool rotated_even() {
 // hi and lo entries. The block sums of x' (for Q4_1/Q5_1) are added over the
 // four lanes of a block. No reduction spans more than one wave.
 //
+// Packed (pk = 1, N <= 8, ncol = 8): the wave of column j writes hi to A row j
+// and lo to A row j + 8 of one plane, the chunk scale to both, and the block
+// sums to row j only (row j + 8 gets 0, so Q4_1/Q5_1 add m * sum x once).
+//
 // A launch split over K adds two partial sums into y, so then (y0 != nullptr)
 // the wave also clears its share of column j of y: rows
 // [ch * per, (ch + 1) * per) with per = ceil(M / chunks).
@@ -127,7 +134,7 @@ __device__ __forceinline__ int qm_wave_or(int v) {  // every lane: OR over the w
 }
 
 __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot,
-                                                   int ncol, float* __restrict__ y0, int64_t ldy, int64_t M,
+                                                   int ncol, int pk, float* __restrict__ y0, int64_t ldy, int64_t M,
                                                    uint8_t* __restrict__ ws) {
     uint4* const xa = (uint4*) ws;
     float* const meta = (float*) (ws + QM_A_BYTES);
@@ -174,13 +181,16 @@ __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, i
     // the 4 lanes of a block (a quad): sum, in every one of them
     sm += __builtin_bit_cast(float, qm_dpp<0xB1, 0xF>(__builtin_bit_cast(int, sm)));
     sm += __builtin_bit_cast(float, qm_dpp<0x4E, 0xF>(__builtin_bit_cast(int, sm)));
+    const float sc = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
     if (b < nblk) {
         uint4* dst = xa + ((int64_t) (j >> 4) * QM_MAX_BLOCKS + b) * 2 * 64 + (j & 15) + 16 * g;
         dst[0] = __builtin_bit_cast(uint4, hi);
-        dst[64] = __builtin_bit_cast(uint4, lo);
+        dst[pk ? 8 : 64] = __builtin_bit_cast(uint4, lo);
         if (g == 0) meta[QM_META_XS + b * QM_COLS + j] = sm;
+        if (pk && g == 0) meta[QM_META_XS + b * QM_COLS + j + 8] = 0.f;
     }
-    if (l == 0) meta[ch * QM_COLS + j] = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
+    if (l == 0) meta[ch * QM_COLS + j] = sc;
+    if (pk && l == 0) meta[ch * QM_COLS + j + 8] = sc;
 }
 
 // Per format: which dwords of a pair each lane loads (NW of them), in bytes
@@ -346,7 +356,8 @@ struct QmX {
     QmXT u[NT];  // column tiles
 };
 
-template <int TYPE, int NT>
+// PK: packed hi/lo (one tile, N <= 8): only plane 0 of each block.
+template <int TYPE, int NT, bool PK>
 __device__ __forceinline__ void qm_load_x(QmX<NT>& x, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rm,
                                           uint32_t ao, uint32_t mo, int p) {
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
@@ -356,7 +367,7 @@ __device__ __forceinline__ void qm_load_x(QmX<NT>& x, __amdgpu_buffer_rsrc_t ra,
         for (int h = 0; h < 2; ++h) {
             const int b = 2 * p + h;
 #pragma unroll
-            for (int pl = 0; pl < 2; ++pl) {
+            for (int pl = 0; pl < (PK ? 1 : 2); ++pl) {
                 x.u[u].a[h][pl] = __builtin_bit_cast(
                     h8, __builtin_amdgcn_raw_buffer_load_b128(ra, ao, ((u * QM_MAX_BLOCKS + b) * 2 + pl) * 1024, 0));
             }
@@ -406,7 +417,7 @@ __device__ __forceinline__ void qm_scale(const f4 (&c)[2], const uint32_t (&dm)[
 // t + 1 and scales tile t - 1, whose MFMA results are one step old. The
 // scheduling barriers keep the compiler from folding the steps back into a
 // dependent chain.
-template <int TYPE, int T, int NT>
+template <int TYPE, int T, int NT, bool PK>
 __device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32_t* lo, const QmX<NT>& x, int g,
                                            uint32_t sel, const QmK& kc, f4 (*acc)[NT]) {
     constexpr int NW = QmFmt<TYPE>::NW, RB = QM_CP * QmFmt<TYPE>::PW * 4;  // bytes of one row in a chunk
@@ -428,11 +439,13 @@ __device__ __forceinline__ void qm_compute(const uint8_t* lds_pair, const uint32
 #pragma unroll
             for (int h = 0; h < 2; ++h)
                 c[t][u][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.u[u].a[h][0], q[t].B[h], zero, 0, 0, 0);
+        if constexpr (!PK) {  // packed: plane 0 already carries lo in rows 8..15
 #pragma unroll
-        for (int u = 0; u < NT; ++u)
+            for (int u = 0; u < NT; ++u)
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-                c[t][u][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.u[u].a[h][1], q[t].B[h], c[t][u][h], 0, 0, 0);
+                for (int h = 0; h < 2; ++h)
+                    c[t][u][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.u[u].a[h][1], q[t].B[h], c[t][u][h], 0, 0, 0);
+        }
         if (t + 1 < T) q[t + 1] = qm_decode<TYPE>(w[t + 1], g, sel, kc);
         if (t >= 1) {
 #pragma unroll
@@ -479,7 +492,10 @@ struct QmTile {
 // K split: blockIdx.y selects chunks [c0, c0 + part_chunks) of K. With more than
 // one part (gridDim.y == 2) the parts' sums meet in y, which k_qmm_xprep
 // cleared, by float atomic adds; 0 + a + b rounds the same in either order.
-template <int TYPE, int T, int ROUNDS, int R, int NT>
+//
+// PK: packed hi/lo x (NT = 1, N <= 8): one x load and one MFMA per block, and
+// result rows j + 8 (the lo products) are added into rows j at the end.
+template <int TYPE, int T, int ROUNDS, int R, int NT, bool PK>
 __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict__ W, int nblk, int64_t M,
                                                         int64_t nb1_w, float* __restrict__ y, int64_t ldy, int N,
                                                         int rows_per_wg, int part_chunks,
@@ -488,7 +504,8 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     constexpr int NW = QmFmt<TYPE>::NW, PW = TL::PW;
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
     // x loads per chunk and wave: per column tile two blocks x two planes, scales, block sums
-    constexpr int NA = NT * (MIN ? 7 : 5);
+    static_assert(!PK || NT == 1, "packed x is one tile of 8 columns");
+    constexpr int NA = NT * ((PK ? 1 : 2) * 2 + 1 + (MIN ? 2 : 0));
     // the chunk ring, reused at the end for the sums of every wave
     constexpr int RED = QM_WAVES * T * NT * 64 * 16;
     constexpr int LDS_BYTES = (R + 1) * TL::BUF > RED ? (R + 1) * TL::BUF : RED;
@@ -562,7 +579,7 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     // x operands of this wave's pair of the part's chunk c -> xr[xs]
     auto load_x = [&](int c, int xs) {
         const int p = (c0 + (c < nl ? c : nl - 1)) * QM_CP + wave;
-        qm_load_x<TYPE, NT>(xr[xs], rx, rm, xo, mo, p < np ? p : np - 1);
+        qm_load_x<TYPE, NT, PK>(xr[xs], rx, rm, xo, mo, p < np ? p : np - 1);
     };
     // Step c. Loads go out per chunk as W then x, so once at most (R - 1) chunks'
     // loads are outstanding, chunk c's W (this wave's part) and x have landed;
@@ -579,7 +596,7 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
         asm volatile("" ::: "memory");
         load_w(c + R, (c + R) % (R + 1));
         if (c < nl && (c0 + c) * QM_CP + wave < np) {
-            qm_compute<TYPE, T, NT>(lds + (c % (R + 1)) * TL::BUF, lo, xr[xs], g, sel, kc, acc);
+            qm_compute<TYPE, T, NT, PK>(lds + (c % (R + 1)) * TL::BUF, lo, xr[xs], g, sel, kc, acc);
         }
         load_x(c + R, xs);
     };
@@ -613,6 +630,13 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
         f4 sum = red[(t * NT + u) * 64 + lane];
 #pragma unroll
         for (int w = 1; w < QM_WAVES; ++w) sum += red[((w * T + t) * NT + u) * 64 + lane];
+        if constexpr (PK) {
+            // lane groups 2 and 3 hold the lo products of lane groups 0 and 1's columns
+            if (lane < 32) {
+#pragma unroll
+                for (int w = 0; w < QM_WAVES; ++w) sum += red[((w * T + t) * NT + u) * 64 + lane + 32];
+            }
+        }
         const int64_t m = r0 + 16 * t + m16;
         if (m >= rend) continue;
         if (gridDim.y == 1) {
@@ -633,11 +657,11 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     }
 }
 
-template <int TYPE, int T, int ROUNDS, int R, int NT>
+template <int TYPE, int T, int ROUNDS, int R, int NT, bool PK>
 int launch_t(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows, int parts,
              int part_chunks, const uint8_t* ws, hipStream_t s) {
     const int64_t grid = (M + rows - 1) / rows;
-    hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R, NT>), dim3((unsigned) grid, (unsigned) parts), dim3(QM_WAVES * 64), 0,
+    hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R, NT, PK>), dim3((unsigned) grid, (unsigned) parts), dim3(QM_WAVES * 64), 0,
                        s, (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, y, (int64_t) (nb1_y / sizeof(float)), N, rows,
                        part_chunks, ws);
     return check_launch("qmm");
@@ -681,32 +705,32 @@ constexpr int qm_max_rows() {
 // ROUNDS = 16-byte LDS pieces of a chunk per thread, rounded up. Rows come in
 // multiples of 8, so T tiles hold 16T - 8 or 16T rows and ROUNDS takes one of
 // two values.
-template <int TYPE, int T, int NT>
+template <int TYPE, int T, int NT, bool PK>
 int launch_rounds(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
                   int parts, int part_chunks, const uint8_t* ws, hipStream_t s) {
     constexpr int LS16 = qm_ls16<TYPE>();
     constexpr int LO = qm_rounds(16 * T - 8, LS16), HI = qm_rounds(16 * T, LS16);
     const int rounds = qm_rounds(rows, LS16);
     if (rounds <= LO) {
-        return launch_t<TYPE, T, LO, qm_ring<TYPE, NT>(T, LO), NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
+        return launch_t<TYPE, T, LO, qm_ring<TYPE, NT>(T, LO), NT, PK>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
                                                                part_chunks, ws, s);
     }
     if constexpr (16 * T <= qm_max_rows<TYPE, NT>()) {  // 16T rows is within the cap
-        return launch_t<TYPE, T, HI, qm_ring<TYPE, NT>(T, HI), NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
+        return launch_t<TYPE, T, HI, qm_ring<TYPE, NT>(T, HI), NT, PK>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
                                                                part_chunks, ws, s);
     } else {
         return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
     }
 }
 
-template <int TYPE, int T, int NT>
+template <int TYPE, int T, int NT, bool PK>
 int launch_tiles(int t, const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
                  int parts, int part_chunks, const uint8_t* ws, hipStream_t s) {
     if constexpr (T > (qm_max_rows<TYPE, NT>() + 15) / 16) {
         return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
     } else {
-        if (t == T) return launch_rounds<TYPE, T, NT>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, ws, s);
-        return launch_tiles<TYPE, T + 1, NT>(t, wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, ws, s);
+        if (t == T) return launch_rounds<TYPE, T, NT, PK>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, ws, s);
+        return launch_tiles<TYPE, T + 1, NT, PK>(t, wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, ws, s);
     }
 }
 
@@ -735,25 +759,28 @@ QmPlan qm_plan(int nblk, int64_t M) {
 }
 
 // NT = 1 for N <= 16, 2 for 17 <= N <= 32: every column tile shares one pass over W.
-template <int TYPE, int NT>
+// PK (N <= 8): x hi and lo packed into one tile.
+template <int TYPE, int NT, bool PK>
 int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
                size_t nb1_y, uint8_t* ws, hipStream_t s) {
     const QmPlan p = qm_plan<TYPE, NT>(nblk, M);
     const int nchunks = (nblk + QM_CHB - 1) / QM_CHB;
-    hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) (nchunks * 16 * NT)), dim3(64), 0, s, x,
-                       (int64_t) (nb1_x / sizeof(float)), N, nblk, rotated_even<TYPE>() ? 2 : 0, 16 * NT,
+    const int ncol = PK ? 8 : 16 * NT;  // one pre-pass wave per chunk and column
+    hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) (nchunks * ncol)), dim3(64), 0, s, x,
+                       (int64_t) (nb1_x / sizeof(float)), N, nblk, rotated_even<TYPE>() ? 2 : 0, ncol, PK ? 1 : 0,
                        p.parts > 1 ? y : nullptr, (int64_t) (nb1_y / sizeof(float)), M, ws);
     const int rc = check_launch("qmm_xprep");
     if (rc != TRC_HIP_OK) return rc;
-    return launch_tiles<TYPE, 1, NT>((p.rows + 15) / 16, wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts,
+    return launch_tiles<TYPE, 1, NT, PK>((p.rows + 15) / 16, wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts,
                                      p.part_chunks, ws, s);
 }
 
 template <int TYPE>
 int launch_cols(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
                 size_t nb1_y, uint8_t* ws, hipStream_t s) {
-    if (N > 16) return launch_fmt<TYPE, 2>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
-    return launch_fmt<TYPE, 1>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
+    if (N > 16) return launch_fmt<TYPE, 2, false>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
+    if (N > 8) return launch_fmt<TYPE, 1, false>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
+    return launch_fmt<TYPE, 1, true>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
 }
 
 }  // namespace
