@@ -109,6 +109,9 @@ def test_backward_goldens(hip, case):
     # 128 or more 128x128 tiles but under 512 and K >= 1024: K in two parts summed
     # by atomic adds (partial tiles, K not a multiple of the slab, two planes)
     (2500, 2000, 1000, 1, 1, 1, 1), (1030, 1000, 1000, 1, 1, 2, 1),
+    # plane counts that are a multiple of 8 (each plane's tiles on one XCD):
+    # ragged 64x64 tiles over 8 planes, ragged 128x128 tiles over 64 planes
+    (33, 70, 90, 4, 2, 1, 1), (40, 300, 300, 8, 8, 1, 1),
 ])
 @pytest.mark.parametrize("layout", ["kk", "tk", "kt", "tt", "gen"])
 def test_random_shapes_and_layouts(hip, shape, layout):

@@ -26,6 +26,11 @@
 //     GENERIC (scalar loads for any other stride). Out-of-range elements load 0.
 //   - The next slab is fetched into registers while the current one is being
 //     multiplied, so global latency overlaps MFMA work.
+//   - Workgroups go to the 8 XCDs in turn (workgroup b on XCD b % 8), each
+//     with its own L2. With a multiple of 8 planes, every tile of plane p is
+//     put on XCD p % 8, so each src1 plane (and, under the modulo broadcast,
+//     each src0 plane) is read into one L2 only; otherwise tiles follow the
+//     grid order, where the tiles sharing one src0 row block meet on one XCD.
 //   - When 128x128 tiles would give under two workgroups per CU, K is split in
 //     two: 8-wave workgroups (64x32 per wave) each sum half of K for one tile,
 //     into a dst cleared beforehand, with float atomic adds. 0 + a + b rounds
@@ -47,6 +52,7 @@ struct MMArgs {
     int64_t b_nb0, b_nb1, b_nb2, b_nb3, b_ne2;
     int64_t d_nb0, d_nb1, d_nb2, d_nb3;
     int64_t tiles_i, tiles_j;
+    int xcd_planes;  // 1: planes % 8 == 0, tiles of plane p on XCD p % 8
 };
 
 // Loads a ROWS x BK slab (rows = i for src0, j for src1) of one operand into
@@ -153,6 +159,11 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
     const int wj = wave / WI;
 
     int64_t t = blockIdx.x;
+    if (p.xcd_planes) {
+        // workgroup b = 8k + x runs on XCD x: give it tile k % tpp of plane 8 (k / tpp) + x
+        const int64_t tpp = p.tiles_i * p.tiles_j * SPLIT, x = t & 7, k = t >> 3;
+        t = (8 * (k / tpp) + x) * tpp + k % tpp;
+    }
     const int part = SPLIT > 1 ? (int) (t % SPLIT) : 0;
     t /= SPLIT;
     const int64_t ti = t % p.tiles_i;
@@ -262,6 +273,7 @@ int launch_cfg(MMArgs& p, int64_t planes, hipStream_t stream) {
     p.tiles_j = (p.N + BN - 1) / BN;
     const int64_t grid = p.tiles_i * p.tiles_j * planes * SPLIT;
     if (grid > 0x7FFFFFFF) return fail(TRC_HIP_E_SHAPE, "mul_mat: %lld workgroups exceed one launch", (long long) grid);
+    p.xcd_planes = planes % 8 == 0 ? 1 : 0;
     hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, BK, AM, BMO, SPLIT>), dim3((unsigned) grid), dim3(WI * WJ * 64), 0,
                        stream, p);
     return check_launch("mul_mat_f32");
