@@ -166,6 +166,29 @@ def test_mfma_grid_shapes(hip, name, M, N):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("K, M, N", [(1024, 7000, 8), (2048, 6500, 5), (768, 9000, 6), (256, 8000, 7),
+                                     (512, 14336, 8), (256, 20000, 8)])
+def test_mfma_x_in_lds(hip, name, K, M, N):
+    """Up to 8 columns with K in one part of at most 4 chunks (M above 24 rows
+    per CU): where x fits beside the chunk ring (32 to 56 rows per workgroup, 80
+    for Q4_0), every workgroup converts x into LDS itself, with no pre-pass; the
+    other formats take the pre-pass. K = 768 ends on a half chunk, K = 256 is one
+    chunk of 4 pairs. A NaN in the last column checks that the in-LDS scales
+    carry it."""
+    t = TYPES[name]
+    announce(f"qmm x in LDS {name} K={K} M={M} N={N}")
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 41 + K + N))
+    X = synth.normal(43 + M, K * N).reshape(1, 1, N, K).astype(np.float32)
+    X[0, 0, 1] *= np.float32(1e-20)  # columns of very different magnitude
+    X[0, 0, 2, 32:64] = np.float32(1e-40)  # a denormal block
+    X[0, 0, N - 1, K - 7] = np.nan
+    got = gpu_qmatvec(t, raw, K, M, X, x_pad=4, y_pad=3)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert not np.isfinite(got[0, 0, N - 1]).any()
+    assert O.row_l2_error(got[:, :, : N - 1], want[:, :, : N - 1]) <= TOL
+
+
+@pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("N", [8, 9])
 def test_mfma_dynamic_range(hip, name, N):
     """Columns of very different magnitude, blocks of very different magnitude

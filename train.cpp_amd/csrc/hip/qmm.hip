@@ -57,7 +57,9 @@
 // the waves through LDS in a fixed order, so results are deterministic. Rows
 // per workgroup are chosen so the grid covers every CU once when M allows;
 // up to 24 rows per CU, K is split in two parts whose sums meet in y by float
-// atomic adds (0 + a + b, the same in either order).
+// atomic adds (0 + a + b, the same in either order). Up to 8 columns with K in
+// one part of at most 4 chunks, each workgroup converts x into LDS itself and
+// the pre-pass does not run.
 #include "common.h"
 
 namespace trc_hip {
@@ -92,20 +94,6 @@ constexpr bool rotated_even() {
     return TYPE == TRC_HIP_TYPE_Q4_0 || TYPE == TRC_HIP_TYPE_Q5_0 || TYPE == TRC_HIP_TYPE_Q8_0;
 }
 
-// One wave per (chunk of QM_CHB blocks, column j < ncol = 16 or 32): lane l carries block
-// b = l / 4 of the chunk and lane group g = l % 4. It loads exactly the 8
-// elements of A entry (b, g) (the low elements e_p and e_p + 16), the wave's
-// largest |x| and finiteness give the chunk's scale 2^s, and the lane writes its
-// hi and lo entries. The block sums of x' (for Q4_1/Q5_1) are added over the
-// four lanes of a block. No reduction spans more than one wave.
-//
-// Packed (pk = 1, N <= 8, ncol = 8): the wave of column j writes hi to A row j
-// and lo to A row j + 8 of one plane, the chunk scale to both, and the block
-// sums to row j only (row j + 8 gets 0, so Q4_1/Q5_1 add m * sum x once).
-//
-// A launch split over K adds two partial sums into y, so then (y0 != nullptr)
-// the wave also clears its share of column j of y: rows
-// [ch * per, (ch + 1) * per) with per = ceil(M / chunks).
 // Wave-wide reductions with DPP row operations (VALU latency, no LDS
 // round trips): within rows of 16, then into lane 63 with the row broadcasts,
 // whose masked-out rows keep 0 (the identity here: values are >= 0, flags 0/1).
@@ -133,27 +121,32 @@ __device__ __forceinline__ int qm_wave_or(int v) {  // every lane: OR over the w
     return __builtin_amdgcn_readlane(v, 63);
 }
 
-__global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot,
-                                                   int ncol, int pk, float* __restrict__ y0, int64_t ldy, int64_t M,
-                                                   uint8_t* __restrict__ ws) {
-    uint4* const xa = (uint4*) ws;
-    float* const meta = (float*) (ws + QM_A_BYTES);
-    const int ch = blockIdx.x / ncol, j = blockIdx.x % ncol;  // columns past N get zeros
-    const int l = threadIdx.x, bl = l >> 2, g = l & 3;
-    if (y0 != nullptr && j < N) {
-        const int64_t nchunks = gridDim.x / ncol, per = (M + nchunks - 1) / nchunks;
-        const int64_t a = ch * per, e = a + per < M ? a + per : M;
-        for (int64_t m = a + l; m < e; m += 64) y0[j * ldy + m] = 0.f;
-    }
+// The 8 x elements lane (block bl = l / 4 of chunk ch, lane group g = l % 4)
+// of the wave for column j converts, in slot order (zeros past N or nblk).
+__device__ __forceinline__ void qm_xload(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot, int ch,
+                                         int j, int l, float2 (&v)[4]) {
+    const int bl = l >> 2, g = l & 3;
     const int b = ch * QM_CHB + bl;
     const bool live = j < N && b < nblk;
     const int c = ((b & 1) == 0 && rot) ? 2 : 0;
     const int e0 = (c + 4 * g) & 15, e2 = (c + 4 * g + 2) & 15;  // e1 = e0 + 1, e3 = e2 + 1
     const float2* blk = (const float2*) (x + (int64_t) (live ? j : 0) * ldx + (int64_t) (live ? b : 0) * QK);
     const float2 z = {0.f, 0.f};
-    const float2 v01 = live ? blk[e0 >> 1] : z, v23 = live ? blk[e2 >> 1] : z;
-    const float2 w01 = live ? blk[(e0 + 16) >> 1] : z, w23 = live ? blk[(e2 + 16) >> 1] : z;
-    const float v[8] = {v01.x, v23.x, w01.x, w23.x, v01.y, v23.y, w01.y, w23.y};  // slot order
+    v[0] = live ? blk[e0 >> 1] : z;
+    v[1] = live ? blk[e2 >> 1] : z;
+    v[2] = live ? blk[(e0 + 16) >> 1] : z;
+    v[3] = live ? blk[(e2 + 16) >> 1] : z;
+}
+
+// One chunk of one column, converted by one wave from the values qm_xload gave
+// each lane: the chunk's scale 2^-s (NaN for a chunk with a non-finite value),
+// the lane's hi and lo A entries and its block's sum of x' (in every lane of the block).
+struct QmXConv {
+    h8 hi, lo;
+    float sm, sc;
+};
+__device__ __forceinline__ QmXConv qm_xconv(const float2 (&w)[4]) {
+    const float v[8] = {w[0].x, w[1].x, w[2].x, w[3].x, w[0].y, w[1].y, w[2].y, w[3].y};  // slot order
     float mx = 0.f;
     int bad = 0;  // fmaxf drops NaN, so non-finite values are flagged separately
 #pragma unroll
@@ -168,29 +161,63 @@ __global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, i
     // 2^-s stays a float: below 2^-135 every x is a multiple of 2^-149, and
     // x * 2^149 is then an exact integer under 2^14.
     const int s = (mx > 0.f && finite) ? min(QM_XBITS - __builtin_amdgcn_frexp_expf(mx), 149) : 0;
-    h8 hi, lo;
+    QmXConv r;
     float sm = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const float e = finite ? __builtin_ldexpf(v[k], s) : 0.f;
         sm += e;
         const _Float16 h = (_Float16) e;
-        hi[k] = h;
-        lo[k] = (_Float16) (e - (float) h);
+        r.hi[k] = h;
+        r.lo[k] = (_Float16) (e - (float) h);
     }
     // the 4 lanes of a block (a quad): sum, in every one of them
     sm += __builtin_bit_cast(float, qm_dpp<0xB1, 0xF>(__builtin_bit_cast(int, sm)));
     sm += __builtin_bit_cast(float, qm_dpp<0x4E, 0xF>(__builtin_bit_cast(int, sm)));
-    const float sc = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
+    r.sm = sm;
+    r.sc = finite ? __builtin_ldexpf(1.f, -s) : __builtin_nanf("");
+    return r;
+}
+
+// One wave per (chunk of QM_CHB blocks, column j < ncol = 16 or 32): lane l carries block
+// b = l / 4 of the chunk and lane group g = l % 4. It loads exactly the 8
+// elements of A entry (b, g) (the low elements e_p and e_p + 16), the wave's
+// largest |x| and finiteness give the chunk's scale 2^s, and the lane writes its
+// hi and lo entries. The block sums of x' (for Q4_1/Q5_1) are added over the
+// four lanes of a block. No reduction spans more than one wave.
+//
+// Packed (pk = 1, N <= 8, ncol = 8): the wave of column j writes hi to A row j
+// and lo to A row j + 8 of one plane, the chunk scale to both, and the block
+// sums to row j only (row j + 8 gets 0, so Q4_1/Q5_1 add m * sum x once).
+//
+// A launch split over K adds two partial sums into y, so then (y0 != nullptr)
+// the wave also clears its share of column j of y: rows
+// [ch * per, (ch + 1) * per) with per = ceil(M / chunks).
+__global__ __launch_bounds__(64) void k_qmm_xprep(const float* __restrict__ x, int64_t ldx, int N, int nblk, int rot,
+                                                   int ncol, int pk, float* __restrict__ y0, int64_t ldy, int64_t M,
+                                                   uint8_t* __restrict__ ws) {
+    uint4* const xa = (uint4*) ws;
+    float* const meta = (float*) (ws + QM_A_BYTES);
+    const int ch = blockIdx.x / ncol, j = blockIdx.x % ncol;  // columns past N get zeros
+    const int l = threadIdx.x, bl = l >> 2, g = l & 3;
+    if (y0 != nullptr && j < N) {
+        const int64_t nchunks = gridDim.x / ncol, per = (M + nchunks - 1) / nchunks;
+        const int64_t a = ch * per, e = a + per < M ? a + per : M;
+        for (int64_t m = a + l; m < e; m += 64) y0[j * ldy + m] = 0.f;
+    }
+    float2 v[4];
+    qm_xload(x, ldx, N, nblk, rot, ch, j, l, v);
+    const QmXConv r = qm_xconv(v);
+    const int b = ch * QM_CHB + bl;
     if (b < nblk) {
         uint4* dst = xa + ((int64_t) (j >> 4) * QM_MAX_BLOCKS + b) * 2 * 64 + (j & 15) + 16 * g;
-        dst[0] = __builtin_bit_cast(uint4, hi);
-        dst[pk ? 8 : 64] = __builtin_bit_cast(uint4, lo);
-        if (g == 0) meta[QM_META_XS + b * QM_COLS + j] = sm;
+        dst[0] = __builtin_bit_cast(uint4, r.hi);
+        dst[pk ? 8 : 64] = __builtin_bit_cast(uint4, r.lo);
+        if (g == 0) meta[QM_META_XS + b * QM_COLS + j] = r.sm;
         if (pk && g == 0) meta[QM_META_XS + b * QM_COLS + j + 8] = 0.f;
     }
-    if (l == 0) meta[ch * QM_COLS + j] = sc;
-    if (pk && l == 0) meta[ch * QM_COLS + j + 8] = sc;
+    if (l == 0) meta[ch * QM_COLS + j] = r.sc;
+    if (pk && l == 0) meta[ch * QM_COLS + j + 8] = r.sc;
 }
 
 // Per format: which dwords of a pair each lane loads (NW of them), in bytes
@@ -482,6 +509,21 @@ struct QmTile {
     static constexpr int BUF = FILL > 16 * T * LS ? FILL : 16 * T * LS;
 };
 
+// k_qmm's LDS: the chunk ring (reused at the end for the sums of every wave),
+// then with LXC > 0 the part's x in LDS: the A entries [block of the part][lane]
+// (16 bytes each), the chunk scales [chunk][slot] and (Q4_1/Q5_1) the block
+// sums [block of the part][slot].
+template <int TYPE, int T, int ROUNDS, int R, int NT, int LXC>
+struct QmLdsX {
+    static constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
+    static constexpr int RING = (R + 1) * QmTile<TYPE, T, ROUNDS>::BUF;
+    static constexpr int RED = QM_WAVES * T * NT * 64 * 16;
+    static constexpr int X0 = RING > RED ? RING : RED;                 // A entries
+    static constexpr int SC0 = X0 + LXC * QM_CHB * 1024;               // chunk scales
+    static constexpr int XS0 = SC0 + LXC * 16 * 4;                     // block sums
+    static constexpr int BYTES = XS0 + (MIN ? LXC * QM_CHB * 16 * 4 : 0);
+};
+
 // R chunks of W stream from HBM straight into an LDS ring of R + 1 buffers
 // (buffer_load ... lds: no registers, no VALU), each chunk with the x operands
 // it needs loaded R chunks ahead into a register ring. Per chunk every wave
@@ -495,22 +537,31 @@ struct QmTile {
 //
 // PK: packed hi/lo x (NT = 1, N <= 8): one x load and one MFMA per block, and
 // result rows j + 8 (the lo products) are added into rows j at the end.
-template <int TYPE, int T, int ROUNDS, int R, int NT, bool PK>
+//
+// LXC > 0 (packed, K in one part of at most LXC chunks): the workgroup converts
+// x (xsrc, columns ldx floats apart) into LDS before the main loop, in the
+// workspace's layout: wave w takes column w, one chunk at a time, as
+// k_qmm_xprep does, and the main loop reads its x operands from LDS. Its x
+// loads are issued before the first W copies, so the in-order vmcnt does not
+// hold them behind the copies. ws is then not read and no pre-pass runs.
+template <int TYPE, int T, int ROUNDS, int R, int NT, bool PK, int LXC>
 __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict__ W, int nblk, int64_t M,
                                                         int64_t nb1_w, float* __restrict__ y, int64_t ldy, int N,
                                                         int rows_per_wg, int part_chunks,
-                                                        const uint8_t* __restrict__ ws) {
+                                                        const uint8_t* __restrict__ ws, const float* __restrict__ xsrc,
+                                                        int64_t ldx) {
     using TL = QmTile<TYPE, T, ROUNDS>;
+    using LL = QmLdsX<TYPE, T, ROUNDS, R, NT, LXC>;
     constexpr int NW = QmFmt<TYPE>::NW, PW = TL::PW;
     constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
+    constexpr bool LX = LXC > 0;
     // x loads per chunk and wave: per column tile two blocks x two planes, scales, block sums
     static_assert(!PK || NT == 1, "packed x is one tile of 8 columns");
-    constexpr int NA = NT * ((PK ? 1 : 2) * 2 + 1 + (MIN ? 2 : 0));
-    // the chunk ring, reused at the end for the sums of every wave
-    constexpr int RED = QM_WAVES * T * NT * 64 * 16;
-    constexpr int LDS_BYTES = (R + 1) * TL::BUF > RED ? (R + 1) * TL::BUF : RED;
-    static_assert(LDS_BYTES <= QM_LDS, "LDS");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+    static_assert(!LX || PK, "x in LDS is the packed layout");
+    static_assert(!LX || QM_WAVES == 8, "one wave per packed column");
+    constexpr int NA = LX ? 0 : NT * ((PK ? 1 : 2) * 2 + 1 + (MIN ? 2 : 0));
+    static_assert(LL::BYTES <= QM_LDS, "LDS");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[LL::BYTES];
 
     // wave index as a scalar: the pair a wave computes and its buffer offsets are wave-uniform
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -596,16 +647,68 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
         asm volatile("" ::: "memory");
         load_w(c + R, (c + R) % (R + 1));
         if (c < nl && (c0 + c) * QM_CP + wave < np) {
-            qm_compute<TYPE, T, NT, PK>(lds + (c % (R + 1)) * TL::BUF, lo, xr[xs], g, sel, kc, acc);
+            if constexpr (LX) {
+                // this wave's pair of local chunk c: blocks c * 16 + 2 * wave + h of the part
+                QmX<NT> xq;
+                const int bq = c * QM_CHB + 2 * wave;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    xq.u[0].a[h][0] = *(const h8*) (lds + LL::X0 + ((bq + h) * 64 + lane) * 16);
+                    if constexpr (MIN) xq.u[0].xs[h] = *(const f4*) (lds + LL::XS0 + ((bq + h) * 16 + 4 * g) * 4);
+                }
+                xq.u[0].sc = *(const f4*) (lds + LL::SC0 + (c * 16 + 4 * g) * 4);
+                qm_compute<TYPE, T, NT, PK>(lds + (c % (R + 1)) * TL::BUF, lo, xq, g, sel, kc, acc);
+            } else {
+                qm_compute<TYPE, T, NT, PK>(lds + (c % (R + 1)) * TL::BUF, lo, xr[xs], g, sel, kc, acc);
+            }
         }
-        load_x(c + R, xs);
+        if constexpr (!LX) load_x(c + R, xs);
     };
+    // x of the part into LDS: loads first, then the W copies, then the conversion
+    float2 xv[LX ? LXC : 1][4];
+    if constexpr (LX) {
+#pragma unroll
+        for (int c = 0; c < LXC; ++c) {
+            if (c < nl) qm_xload(xsrc, ldx, N, nblk, rotated_even<TYPE>() ? 2 : 0, c0 + c, wave, lane, xv[c]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // prologue in chunk order (the first wait counts on chunk 0's loads being the oldest)
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         load_w(i, i);
-        load_x(i, i);
+        if constexpr (!LX) load_x(i, i);
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (LX) {
+        const int bl = lane >> 2, gq = lane & 3, j = wave;
+#pragma unroll
+        for (int c = 0; c < LXC; ++c) {
+            if (c < nl) {
+                const QmXConv r = qm_xconv(xv[c]);
+                uint4* xa = (uint4*) (lds + LL::X0) + (c * QM_CHB + bl) * 64 + j + 16 * gq;
+                xa[0] = __builtin_bit_cast(uint4, r.hi);
+                xa[8] = __builtin_bit_cast(uint4, r.lo);
+                if (lane == 0) {
+                    float* sc = (float*) (lds + LL::SC0) + c * 16;
+                    sc[j] = r.sc;
+                    sc[j + 8] = r.sc;
+                }
+                if constexpr (MIN) {
+                    if (gq == 0) {
+                        float* xs = (float*) (lds + LL::XS0) + (c * QM_CHB + bl) * 16;
+                        xs[j] = r.sm;
+                        xs[j + 8] = 0.f;
+                    }
+                }
+            }
+        }
+        // the LDS writes complete (lgkmcnt; the W copies stay in flight), then every wave's are visible
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     }
     // whole groups of R steps, so that every path issues the same loads (steps
     // past the last chunk compute nothing) and the compiler's own wait counts
@@ -657,14 +760,35 @@ __global__ __launch_bounds__(QM_WAVES * 64) void k_qmm(const uint8_t* __restrict
     }
 }
 
-template <int TYPE, int T, int ROUNDS, int R, int NT, bool PK>
-int launch_t(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows, int parts,
-             int part_chunks, const uint8_t* ws, hipStream_t s) {
-    const int64_t grid = (M + rows - 1) / rows;
-    hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R, NT, PK>), dim3((unsigned) grid, (unsigned) parts), dim3(QM_WAVES * 64), 0,
-                       s, (const uint8_t*) wq, nblk, M, (int64_t) nb1_w, y, (int64_t) (nb1_y / sizeof(float)), N, rows,
-                       part_chunks, ws);
-    return check_launch("qmm");
+// One call's arguments on their way to the launch.
+struct QmCall {
+    const void* wq;
+    int nblk;
+    int64_t M;
+    size_t nb1_w;
+    float* y;
+    size_t nb1_y;
+    int N;
+    int rows, parts, part_chunks;
+    const uint8_t* ws;
+    const float* x;  // read by the kernel only when it converts x itself
+    size_t nb1_x;
+    hipStream_t s;
+};
+
+template <int TYPE, int T, int ROUNDS, int R, int NT, bool PK, int LXC>
+int launch_t(const QmCall& q) {
+    if constexpr (QmLdsX<TYPE, T, ROUNDS, R, NT, LXC>::BYTES > QM_LDS) {
+        // not reached: qm_lx_fits keeps such plans on the pre-pass path
+        return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup and x exceed the LDS", q.rows);
+    } else {
+        const int64_t grid = (q.M + q.rows - 1) / q.rows;
+        hipLaunchKernelGGL((k_qmm<TYPE, T, ROUNDS, R, NT, PK, LXC>), dim3((unsigned) grid, (unsigned) q.parts),
+                           dim3(QM_WAVES * 64), 0, q.s, (const uint8_t*) q.wq, q.nblk, q.M, (int64_t) q.nb1_w, q.y,
+                           (int64_t) (q.nb1_y / sizeof(float)), q.N, q.rows, q.part_chunks, q.ws, q.x,
+                           (int64_t) (q.nb1_x / sizeof(float)));
+        return check_launch("qmm");
+    }
 }
 
 // 16-byte LDS pieces of one row's chunk: the row and one spare.
@@ -705,32 +829,30 @@ constexpr int qm_max_rows() {
 // ROUNDS = 16-byte LDS pieces of a chunk per thread, rounded up. Rows come in
 // multiples of 8, so T tiles hold 16T - 8 or 16T rows and ROUNDS takes one of
 // two values.
-template <int TYPE, int T, int NT, bool PK>
-int launch_rounds(const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
-                  int parts, int part_chunks, const uint8_t* ws, hipStream_t s) {
+template <int TYPE, int T>
+constexpr int qm_rounds_used(int rows) {
+    return qm_rounds(rows, qm_ls16<TYPE>()) <= qm_rounds(16 * T - 8, qm_ls16<TYPE>()) ? qm_rounds(16 * T - 8, qm_ls16<TYPE>())
+                                                                                   : qm_rounds(16 * T, qm_ls16<TYPE>());
+}
+template <int TYPE, int T, int NT, bool PK, int LXC>
+int launch_rounds(const QmCall& q) {
     constexpr int LS16 = qm_ls16<TYPE>();
     constexpr int LO = qm_rounds(16 * T - 8, LS16), HI = qm_rounds(16 * T, LS16);
-    const int rounds = qm_rounds(rows, LS16);
-    if (rounds <= LO) {
-        return launch_t<TYPE, T, LO, qm_ring<TYPE, NT>(T, LO), NT, PK>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
-                                                               part_chunks, ws, s);
-    }
+    if (qm_rounds(q.rows, LS16) <= LO) return launch_t<TYPE, T, LO, qm_ring<TYPE, NT>(T, LO), NT, PK, LXC>(q);
     if constexpr (16 * T <= qm_max_rows<TYPE, NT>()) {  // 16T rows is within the cap
-        return launch_t<TYPE, T, HI, qm_ring<TYPE, NT>(T, HI), NT, PK>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts,
-                                                               part_chunks, ws, s);
+        return launch_t<TYPE, T, HI, qm_ring<TYPE, NT>(T, HI), NT, PK, LXC>(q);
     } else {
-        return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
+        return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", q.rows);
     }
 }
 
-template <int TYPE, int T, int NT, bool PK>
-int launch_tiles(int t, const void* wq, int nblk, int64_t M, size_t nb1_w, float* y, size_t nb1_y, int N, int rows,
-                 int parts, int part_chunks, const uint8_t* ws, hipStream_t s) {
+template <int TYPE, int T, int NT, bool PK, int LXC>
+int launch_tiles(int t, const QmCall& q) {
     if constexpr (T > (qm_max_rows<TYPE, NT>() + 15) / 16) {
-        return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", rows);
+        return fail(TRC_HIP_E_INVALID, "qmm: %d rows per workgroup exceed the LDS plan", q.rows);
     } else {
-        if (t == T) return launch_rounds<TYPE, T, NT, PK>(wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, ws, s);
-        return launch_tiles<TYPE, T + 1, NT, PK>(t, wq, nblk, M, nb1_w, y, nb1_y, N, rows, parts, part_chunks, ws, s);
+        if (t == T) return launch_rounds<TYPE, T, NT, PK, LXC>(q);
+        return launch_tiles<TYPE, T + 1, NT, PK, LXC>(t, q);
     }
 }
 
@@ -758,12 +880,51 @@ QmPlan qm_plan(int nblk, int64_t M) {
     return p;
 }
 
+// x converted inside k_qmm (packed calls with K in one part): at most QM_LXC
+// chunks, i.e. 64 KB of A entries per workgroup beside the chunk ring. With a
+// K split the parts would need y cleared by a launch of its own, which measured
+// slower than the pre-pass (configuration 0 10.8 -> 11.5 us).
+constexpr int QM_LXC = 4;
+
+// Whether the plan's kernel fits the LDS with the part's x beside its ring
+// (QmLdsX with LXC = QM_LXC, at the ROUNDS and ring depth launch_rounds picks).
+template <int TYPE, int T>
+bool qm_lx_fits_t(int rows) {
+    constexpr bool MIN = TYPE == TRC_HIP_TYPE_Q4_1 || TYPE == TRC_HIP_TYPE_Q5_1;
+    const int ro = qm_rounds_used<TYPE, T>(rows);
+    const int ring = (qm_ring<TYPE, 1>(T, ro) + 1) * qm_buf<TYPE>(T, ro);
+    const int red = QM_WAVES * T * 64 * 16;
+    const int bytes = (ring > red ? ring : red) + QM_LXC * QM_CHB * 1024 + QM_LXC * 16 * 4 +
+                      (MIN ? QM_LXC * QM_CHB * 16 * 4 : 0);
+    return bytes <= QM_LDS;
+}
+template <int TYPE>
+bool qm_lx_fits(const QmPlan& p) {
+    if (p.parts != 1 || p.part_chunks > QM_LXC) return false;
+    switch ((p.rows + 15) / 16) {
+        case 1: return qm_lx_fits_t<TYPE, 1>(p.rows);
+        case 2: return qm_lx_fits_t<TYPE, 2>(p.rows);
+        case 3: return qm_lx_fits_t<TYPE, 3>(p.rows);
+        case 4: return qm_lx_fits_t<TYPE, 4>(p.rows);
+        case 5: return qm_lx_fits_t<TYPE, 5>(p.rows);
+        case 6: return qm_lx_fits_t<TYPE, 6>(p.rows);
+        case 7: return qm_lx_fits_t<TYPE, 7>(p.rows);
+        default: return false;
+    }
+}
+
 // NT = 1 for N <= 16, 2 for 17 <= N <= 32: every column tile shares one pass over W.
-// PK (N <= 8): x hi and lo packed into one tile.
+// PK (N <= 8): x hi and lo packed into one tile; with K in one part whose x fits
+// beside the ring, each workgroup converts x itself and no pre-pass runs.
 template <int TYPE, int NT, bool PK>
 int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
                size_t nb1_y, uint8_t* ws, hipStream_t s) {
     const QmPlan p = qm_plan<TYPE, NT>(nblk, M);
+    const QmCall q{wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts, p.part_chunks, ws, x, nb1_x, s};
+    const int tiles = (p.rows + 15) / 16;
+    if constexpr (PK) {
+        if (qm_lx_fits<TYPE>(p)) return launch_tiles<TYPE, 1, NT, PK, QM_LXC>(tiles, q);
+    }
     const int nchunks = (nblk + QM_CHB - 1) / QM_CHB;
     const int ncol = PK ? 8 : 16 * NT;  // one pre-pass wave per chunk and column
     hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) (nchunks * ncol)), dim3(64), 0, s, x,
@@ -771,8 +932,7 @@ int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x
                        p.parts > 1 ? y : nullptr, (int64_t) (nb1_y / sizeof(float)), M, ws);
     const int rc = check_launch("qmm_xprep");
     if (rc != TRC_HIP_OK) return rc;
-    return launch_tiles<TYPE, 1, NT, PK>((p.rows + 15) / 16, wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts,
-                                     p.part_chunks, ws, s);
+    return launch_tiles<TYPE, 1, NT, PK, 0>(tiles, q);
 }
 
 template <int TYPE>
