@@ -1327,6 +1327,17 @@ int launch_dot_one(const uint8_t* w, int64_t nblk, int64_t M, size_t nb1_w, cons
         }
     }
     if (dma) {
+        // Q4_0, one column, K of exactly one 4096-element chunk, 7 or 8 rows per
+        // wave: three rows in flight measured 0.3-0.8 % faster than two (M = 13000,
+        // 14336, 16384; same bits), but 5 % slower at 4 rows per wave and 0.7 %
+        // slower at K = 2048, so only there
+        if constexpr (ONE && NC == 1 && TYPE == TRC_HIP_TYPE_Q4_0 && RPW >= 7) {
+            if (nblk == QD_CH) {
+                hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true, 3, qd_pstore(TYPE, NC, true, ONE), ONE>), g, b,
+                                   0, s, w, nblk, M, (int64_t) nb1_w, x, ldx, y, ldy);
+                return check_launch("qmatvec_dot");
+            }
+        }
         constexpr int PF = qd_prefetch(TYPE, NC, true, false);
         hipLaunchKernelGGL((k_qmatvec_dot<TYPE, RPW, NC, true, PF, qd_pstore(TYPE, NC, true, ONE), ONE>), g, b, 0, s, w,
                            nblk, M, (int64_t) nb1_w, x, ldx, y, ldy);
