@@ -377,3 +377,35 @@ def test_two_streams_do_not_share_x(hip):
             d.free()
     for s in streams:
         s.close()
+
+
+def _random_cases(n=48, seed=20261202):
+    """Seeded shapes across every routing of trc_hip_qmatvec: K with block counts
+    that are and are not multiples of 8 (LDS copies or register loads, matrix
+    cores or not), one to four chunks, M from a handful of rows to more
+    workgroups than CUs (K split or not), N from 1 to 64 (integer-dot kernel,
+    packed and unpacked matrix-core tiles, 32-column slices), padded x and y
+    strides. Sizes keep the oracle under a few seconds in all."""
+    rng = np.random.default_rng(seed)
+    names = list(TYPES)
+    cases = []
+    while len(cases) < n:
+        nblk = int(rng.choice([8, 16, 24, 40, 64, 72, 128, 136, 200, 256, 264, 448])) + int(rng.choice([0, 0, 0, 1, 3]))
+        K = 32 * nblk
+        N = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 24, 31, 32, 33, 40, 48, 64]))
+        M = int(rng.choice([1, 7, 33, 257, 1000, 2049, 4097, 6200, 9000, 14336, 17000]))
+        if K * M * N > 3e8:
+            continue
+        cases.append((names[int(rng.integers(len(names)))], K, M, N, int(rng.integers(0, 3)) * 4, int(rng.integers(0, 3))))
+    return cases
+
+
+@pytest.mark.parametrize("name, K, M, N, x_pad, y_pad", _random_cases())
+def test_random_routes(hip, name, K, M, N, x_pad, y_pad):
+    t = TYPES[name]
+    announce(f"qmatvec random {name} K={K} M={M} N={N} pads={x_pad},{y_pad}")
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, K + 3 * M + 7 * N))
+    X = synth.normal(K * 5 + M + N, K * N).reshape(1, 1, N, K)
+    got = gpu_qmatvec(t, raw, K, M, X, x_pad=x_pad, y_pad=y_pad)
+    want = oracle_qmatvec(t, raw, K, M, X)
+    assert O.row_l2_error(got, want) <= TOL
