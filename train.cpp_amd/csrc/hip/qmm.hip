@@ -18,11 +18,11 @@
 // one fused multiply-add by d per output, and each pair's sum is scaled back by
 // its chunk's 2^-s once. Up to 8 columns, hi and lo share one 16-column tile
 // instead (packed: rows 0..7 of the A operand hold hi of columns 0..7, rows
-// 8..15 their lo), so each block takes one MFMA and one x load; rows j and j + 8
-// of the result are added once at the end. An element keeps ~22 bits of its own magnitude down to
-// 2^17 below its chunk's largest |x|; below that its absolute error stays under
-// 2^-39 of that largest |x|, so outputs carry FP32-level error. A chunk holding
-// Inf or NaN makes its column come out NaN. (One scale per column would save
+// 8..15 their lo), so each block takes one MFMA and one x load; rows j and
+// j + 8 of the result are added once at the end. An element keeps ~22 bits of
+// its own magnitude down to 2^17 below its chunk's largest |x|; below that its
+// absolute error stays under 2^-39 of that largest |x|, so outputs carry
+// FP32-level error. A chunk holding Inf or NaN makes its column come out NaN. (One scale per column would save
 // the per-pair rescaling, but finding a column's largest |x| takes one
 // workgroup per column, which made the pre-pass ~2 us slower than the
 // rescaling saves.)
