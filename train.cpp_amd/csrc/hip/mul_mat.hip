@@ -208,6 +208,11 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
             la.load(a, p.a_nb0, p.a_nb1, i0, p.M, (kt0 + kt + 1) * BK, p.K, tid);
             lb.load(b, p.b_nb0, p.b_nb1, j0, p.N, (kt0 + kt + 1) * BK, p.K, tid);
         }
+        // Several 4-wave workgroups share a CU without a K split: a wave in its
+        // MFMA block issues ahead of the others' loads, stores and barriers
+        // (dW 142 -> 136 us, configuration 4 168 -> 161 us, same bits). The split
+        // products run one workgroup per CU, where it measured no gain.
+        if constexpr (SPLIT == 1) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int s = 0; s < BK / 2; ++s) {
             const int kr = 2 * s + half;
@@ -222,6 +227,7 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
                 for (int y = 0; y < TJ; ++y)
                     acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[y], av[x], acc[x][y], 0, 0, 0);
         }
+        if constexpr (SPLIT == 1) __builtin_amdgcn_s_setprio(0);
         if (more) {
             __syncthreads();
             la.store(As, tid);
