@@ -59,7 +59,7 @@ def test_config2_decode_shapes(hip, name, N):
 @pytest.mark.parametrize("N", [1, 2, 3, 4])
 @pytest.mark.parametrize("K,M,w_off", [(32 * 130, 3001, 0), (32 * 264, 999, 4), (32 * 264, 999, 0), (512, 20000, 0),
                                        (32 * 200, 777, 0), (16384, 300, 0), (32 * 126, 1000, 0), (4096, 3001, 0),
-                                       (4096, 14000, 0), (4096, 16384, 0)])
+                                       (4096, 13001, 0), (4096, 14000, 0), (4096, 16384, 0)])
 def test_dot_kernel_weight_paths(hip, name, N, K, M, w_off):
     """The one- to four-column kernels' ways of reading W (three and four
     columns only through LDS, four only within one chunk and not for Q4_0; the
@@ -71,8 +71,9 @@ def test_dot_kernel_weight_paths(hip, name, N, K, M, w_off):
     LDS with more workgroups than CUs (20000 rows of 8 per wave), and with K in
     one chunk (the instance without the chunk loop, where rows are stored when
     a wave issues its last copies): two rows per wave with one in flight (3001
-    rows), seven rows per wave with rows past M (14000) and eight (16384; Q4_0
-    with one column keeps three rows in flight at both)."""
+    rows), seven rows per wave (14000 rows, and 13001: 233 workgroups whose
+    last rows lie past M) and eight (16384; Q4_0 with one column keeps three
+    rows in flight at all three)."""
     t = TYPES[name]
     announce(f"qmatvec dot paths {name} N={N} K={K} M={M} w_off={w_off}")
     raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 1000 + K + M))
