@@ -20,11 +20,13 @@ bracket each timed replay of the K launches, and the headline is the median
 over --replays replays (the spread is reported beside it). Inputs rotate over buffer sets totalling more
 than 512 MB so the 256 MB Infinity Cache cannot hold them between steps.
 
-cpu_baseline: the reference CPU path (dequantize the whole weight, then the
-serial mul_mat loop) restated in oracle/ and run single-threaded on this
-host's cores for the headline workload; extra.cpu_baseline_all_cores runs it
-on every core this process may use (sched_getaffinity), and extra.host names
-the CPU model.
+cpu_baseline: the reference's own CPU path for the headline workload, compiled
+from its sources into oracle/_ref (gguf_tensor_to_f32 into the F32 weight, then
+mul_mat on its serial CPU Device), on one host core (kind "reference"; its y is
+checked bit for bit against the oracle). Where oracle/_ref is absent, the
+oracle's restatement of the same path (kind "port"). extra.cpu_baseline_port
+times the restatement on one core, extra.cpu_baseline_all_cores on every core
+this process may use (sched_getaffinity), and extra.host names the CPU model.
 """
 from __future__ import annotations
 
@@ -298,6 +300,30 @@ def cpu_baseline(blk: np.ndarray, x: np.ndarray, K: int, M: int, budget_s: float
                       f"{threads} thread{'s' if threads > 1 else ''}"}
 
 
+def cpu_baseline_reference(blk: np.ndarray, x: np.ndarray, K: int, M: int, budget_s: float):
+    """The reference's own CPU path for the headline workload (oracle/_ref, built
+    from its sources): gguf_tensor_to_f32 of the Q4_0 weight into the F32
+    tensor's CPU buffer, then mul_mat on the reference CPU Device, repeated for
+    budget_s seconds on one thread. None where oracle/_ref is absent. Its y must
+    equal the oracle's bit for bit."""
+    import tempfile
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+    if not O.have_ref():
+        return None
+    with tempfile.TemporaryDirectory() as d:
+        y, dt, reps = O.ref_headline(2, blk, x, K, M, budget_s, os.path.join(d, "w.gguf"))
+    W = O.dequant(2, blk, threads=8).reshape(1, 1, M, K)
+    want = O.mul_mat(W, x.reshape(1, 1, 1, K), threads=8).reshape(-1)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32)), "reference path differs from the oracle"
+    alg = blk.nbytes + x.nbytes + M * 4
+    return {"value": alg / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "reference",
+            "sample": f"full headline workload (Q4_0 W[4096,14336] to F32 by the reference's gguf_tensor_to_f32, "
+                      f"then mul_mat with x[4096,1] on its CPU Device), {reps} repetitions, {dt * 1e3:.1f} ms "
+                      f"each, reference sources built by oracle/Makefile (-O3 -std=c++20, no -march), 1 thread; "
+                      f"y bit-identical to the oracle"}
+
+
 def cpu_host_info() -> dict:
     model = "unknown"
     try:
@@ -546,7 +572,12 @@ def main():
         extra["gguf_load_cfg0_hip_route"] = gguf_load_cfg0(H, synth)
 
     host = cpu_host_info()
-    cpu = cpu_baseline(blk, x, K, M, args.cpu_budget)
+    port = cpu_baseline(blk, x, K, M, args.cpu_budget / 2)
+    cpu = cpu_baseline_reference(blk, x, K, M, args.cpu_budget)
+    if cpu is None:
+        cpu = port
+    else:
+        extra["cpu_baseline_port"] = port
     cpu["cpu_model"] = host["cpu_model"]
     extra["cpu_vs_gpu_speedup"] = head["GB/s"] / cpu["value"]
     extra["host"] = host

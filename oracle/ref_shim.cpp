@@ -2,7 +2,8 @@
 // with the reference's own sources (under /root/reference, never copied) into
 // oracle/_ref/libtrc_ref.so by oracle/Makefile. TEST INFRASTRUCTURE ONLY: it lets
 // the CPU tests check the oracle restatement (oracle.cpp) against the code it
-// restates. Nothing in the product loads it.
+// restates, and bench.py's cpu_baseline leg time the reference's own CPU path.
+// Nothing in the product loads it.
 //
 // Entry points go through the same public calls a traincpp user makes:
 //   ref_dequant   -> gguf_open + gguf_tensor_to_f32   (src/io/trc_gguf.cpp:748,966)
@@ -16,11 +17,16 @@
 //                    (src/ops/trc_ops.cpp:458, src/backends/cpu/trc_cpu_ops.cpp:932)
 //   ref_mul / ref_sum / ref_repeat -> permute views + mul / sum / repeat + CPU
 //                    Device (src/ops/trc_ops.cpp:59,214,447; trc_cpu_ops.cpp:52,302,913)
+//   ref_headline_time -> gguf_open + gguf_tensor_to_f32 into the F32 weight's
+//                    CPU buffer, then mul_mat on the CPU Device, repeated and
+//                    timed (the CPU path the fused matvec replaces; bench.py's
+//                    cpu_baseline leg)
 //   ref_fp16_*    -> core/trc_float.h:23-63
 //   ref_rng_*     -> src/core/trc_rng.cpp:38-68
 #include "traincpp/traincpp.h"
 #include "core/trc_float.h"
 
+#include <chrono>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -105,6 +111,81 @@ int ref_dequant(int type, const void* blocks, int64_t n_blocks, float* out, cons
     gguf_close(g);
     std::remove(tmp_path);
     return ok ? 0 : -4;
+}
+
+// The headline workload on the reference's CPU path: W (n = K*M elements of
+// `type` blocks, written once to a GGUF v3 file at tmp_path and opened with its
+// data section loaded) is dequantized by gguf_tensor_to_f32 straight into the
+// CPU buffer of an F32 tensor [K, M], and y = mul_mat(W, x) runs on the CPU
+// Device (graph built and buffers allocated once). After one untimed pass the
+// two steps repeat for at least budget_s seconds. Returns the mean seconds per
+// repetition (negative on an error), y (M floats) and the repetition count.
+double ref_headline_time(int type, const void* blocks, int64_t K, int64_t M, const float* x, float* y,
+                         double budget_s, int* reps_out, const char* tmp_path) {
+    const int64_t n = K * M;
+    const size_t bsz = type_size((Type) type);
+    if (bsz == 0 || n <= 0 || n % 32 != 0) return -1.0;
+    {
+        std::vector<uint8_t> f;
+        put(f, "GGUF", 4);
+        put_pod<uint32_t>(f, 3);
+        put_pod<uint64_t>(f, 1);  // tensors
+        put_pod<uint64_t>(f, 0);  // kvs
+        put_pod<uint64_t>(f, 1);
+        f.push_back('w');
+        put_pod<uint32_t>(f, 1);
+        put_pod<int64_t>(f, n);
+        put_pod<uint32_t>(f, (uint32_t) type);
+        put_pod<uint64_t>(f, 0);
+        pad32(f);
+        put(f, blocks, bsz * (size_t) (n / 32));
+        pad32(f);
+        std::FILE* fp = std::fopen(tmp_path, "wb");
+        if (!fp) return -2.0;
+        const bool wrote = std::fwrite(f.data(), 1, f.size(), fp) == f.size();
+        std::fclose(fp);
+        if (!wrote) return -2.0;
+    }
+    GgufFile* g = gguf_open(tmp_path, true);
+    std::remove(tmp_path);
+    if (!g) return -3.0;
+    Device* dev = device_cpu();
+    if (!dev) {
+        gguf_close(g);
+        return -4.0;
+    }
+    Context* ctx = context_new(1 << 20);
+    Tensor* w = new_tensor_2d(ctx, TYPE_F32, K, M);
+    Tensor* xt = new_tensor_2d(ctx, TYPE_F32, K, 1);
+    Tensor* r = mul_mat(ctx, w, xt);
+    Graph* gr = graph_new(ctx);
+    graph_build_forward_expand(ctx, gr, r);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    tensor_set(xt, x, 0, tensor_nbytes(xt));
+    double result = -5.0;
+    if (w->data != nullptr) {
+        auto pass = [&]() { return gguf_tensor_to_f32(g, "w", (float*) w->data, n) && dev->graph_compute(gr); };
+        bool ok = pass();  // untimed: touches every page
+        int reps = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        double el = 0.0;
+        while (ok) {
+            ok = pass();
+            ++reps;
+            el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            if (el >= budget_s) break;
+        }
+        if (ok) {
+            tensor_get(r, y, 0, tensor_nbytes(r));
+            *reps_out = reps;
+            result = el / reps;
+        }
+    }
+    buffer_free(buf);
+    graph_free(gr);
+    context_free(ctx);
+    gguf_close(g);
+    return result;
 }
 
 // d = mul_mat(permute(A, pa), permute(B, pb)) on the reference CPU device.

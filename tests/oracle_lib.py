@@ -100,6 +100,8 @@ def ref() -> C.CDLL:
         lib.ref_rng_uniform01.restype = F
         lib.ref_rng_normal.argtypes = [C.POINTER(C.c_uint64), F, F]
         lib.ref_rng_normal.restype = F
+        lib.ref_headline_time.argtypes = [I, P, I64, I64, P, P, C.c_double, C.POINTER(I), C.c_char_p]
+        lib.ref_headline_time.restype = C.c_double
         _ref = lib
     return _ref
 
@@ -114,6 +116,22 @@ def dequant(type_: int, blocks: np.ndarray, threads: int = 1) -> np.ndarray:
     rc = oracle().orc_dequant(type_, raw.ctypes.data, n, out.ctypes.data, threads)
     assert rc == 0
     return out
+
+
+def ref_headline(type_: int, blocks: np.ndarray, x: np.ndarray, K: int, M: int, budget_s: float,
+                 tmp_path: str) -> tuple[np.ndarray, float, int]:
+    """The reference's own CPU path for y = W x with W quantized (gguf_tensor_to_f32
+    into the F32 weight, then mul_mat on its CPU Device), repeated for budget_s
+    seconds: returns y, mean seconds per repetition and the repetition count."""
+    raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+    xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    assert xv.size == K
+    y = np.empty(M, dtype=np.float32)
+    reps = I(0)
+    dt = ref().ref_headline_time(type_, raw.ctypes.data, K, M, xv.ctypes.data, y.ctypes.data, budget_s,
+                                 C.byref(reps), tmp_path.encode())
+    assert dt > 0, f"ref_headline_time failed ({dt})"
+    return y, dt, reps.value
 
 
 def ref_dequant(type_: int, blocks: np.ndarray, tmp_dir: str) -> np.ndarray:

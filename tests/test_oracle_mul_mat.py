@@ -157,3 +157,20 @@ def test_threads_split_rows_without_changing_bits():
     one = O.mul_mat(A, B, threads=1)
     for t in (2, 7, 16):
         assert np.array_equal(O.mul_mat(A, B, threads=t).view(np.uint32), one.view(np.uint32))
+
+
+@pytest.mark.skipif(not O.have_ref(), reason="oracle/_ref not built (reference checkout absent)")
+@pytest.mark.parametrize("t", [2, 6, 8])
+def test_reference_headline_path_matches_oracle(t, tmp_path):
+    """The timed reference path that bench.py's CPU baseline runs
+    (gguf_tensor_to_f32 into the weight's CPU buffer, then mul_mat on the
+    reference CPU Device) gives the oracle's dequantize-then-mul_mat bit for bit."""
+    from traincpp_amd import synth
+    K, M = 256, 40
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 50 + t))
+    x = synth.normal(51, K).astype(np.float32)
+    y, dt, reps = O.ref_headline(t, raw, x, K, M, 0.0, str(tmp_path / "w.gguf"))
+    assert reps >= 1 and dt > 0
+    W = O.dequant(t, raw).reshape(1, 1, M, K)
+    want = O.mul_mat(W, x.reshape(1, 1, 1, K)).reshape(-1)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
