@@ -338,33 +338,46 @@ def cpu_host_info() -> dict:
 
 def gguf_load_cfg0_reference_route(H, synth, threads: int, reps: int = 5):
     """The reference's gguf_load_tensor route for configuration 0 on this host:
-    dequantize the Q8_0 blocks on the host (its serial loops, restated in
-    oracle/, 1 thread) into an F32 vector, then upload the 64 MiB F32 weight."""
+    dequantize the Q8_0 blocks on the host into an F32 vector, then upload the
+    64 MiB F32 weight. The dequant is the reference's own gguf_tensor_to_f32
+    (oracle/_ref, 1 thread, mean over ~1 s) where it is built, else the oracle's
+    restatement; the upload is timed here (median of `reps`)."""
+    import tempfile
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as O
-    lib = O.oracle()
     K = M = 4096
     n = K * M // 32
     raw = synth.block_bytes(synth.quant_blocks(H.TYPE_Q8_0, n, synth.config_seed(0, 8)))
+    if O.have_ref():
+        with tempfile.TemporaryDirectory() as d:
+            f32, dq, _ = O.ref_dequant_timed(H.TYPE_Q8_0, raw, 1.0, os.path.join(d, "w.gguf"))
+        code = "reference gguf_tensor_to_f32 (oracle/_ref)"
+    else:
+        f32 = np.empty(K * M, np.float32)
+        t0 = time.perf_counter()
+        assert O.oracle().orc_dequant(H.TYPE_Q8_0, raw.ctypes.data, n, f32.ctypes.data, threads) == 0
+        dq = time.perf_counter() - t0
+        code = "oracle/oracle.cpp"
     w = H.DeviceBuffer(K * M * 4)
     times = []
     for r in range(reps + 1):
         t0 = time.perf_counter()
-        f32 = np.empty(K * M, np.float32)
-        assert lib.orc_dequant(H.TYPE_Q8_0, raw.ctypes.data, n, f32.ctypes.data, threads) == 0
         w.upload(f32)
         times.append(time.perf_counter() - t0)
     w.free()
-    return {"ms": float(np.median(times[1:])) * 1e3, "threads": threads,
-            "sample": "Q8_0 4096x4096 blocks in memory -> host dequant (oracle/oracle.cpp) -> 64 MiB H2D"}
+    up = float(np.median(times[1:]))
+    return {"ms": (dq + up) * 1e3, "dequant_ms": dq * 1e3, "upload_ms": up * 1e3, "threads": 1,
+            "sample": f"Q8_0 4096x4096 blocks in memory -> host dequant ({code}) -> 64 MiB H2D"}
 
 
 def cpu_other_paths(synth, budget_s: float, threads: int):
-    """The reference CPU path of the other two hot paths on this host, one thread
-    and `threads` threads (same bits): H1 = gguf_tensor_to_f32's quant branch on
-    configuration 1's Q4_0 blocks, in memory; H3 = configuration 3's forward
-    product on a bounded slice of 8 of its 512 output columns (1/64), extrapolated
-    to the whole product."""
+    """The reference CPU path of the other two hot paths on this host: H1 =
+    gguf_tensor_to_f32's quant branch on configuration 1's Q4_0 blocks, in
+    memory; H3 = configuration 3's forward product on a bounded slice of 8 of
+    its 512 output columns (1/64), extrapolated to the whole product. One thread
+    runs the reference's own code (oracle/_ref, where built; "code": "reference"),
+    `threads` threads the oracle's restatement split over threads (same bits;
+    "code": "port")."""
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as O
     lib = O.oracle()
@@ -379,13 +392,20 @@ def cpu_other_paths(synth, budget_s: float, threads: int):
             if time.perf_counter() - t0 >= budget_s:
                 return (time.perf_counter() - t0) / reps, reps
 
+    import tempfile
+    ref = O.have_ref()
     n = 4096 * 11008 // 32
     blk = synth.block_bytes(synth.quant_blocks(2, n, synth.config_seed(1, 2)))
     wf = np.empty(n * 32, dtype=np.float32)
     for nt in sorted({1, threads}):
-        dt, reps = timed(lambda nt=nt: lib.orc_dequant(2, blk.ctypes.data, n, wf.ctypes.data, nt))
+        if nt == 1 and ref:  # the reference's own serial gguf_tensor_to_f32
+            with tempfile.TemporaryDirectory() as d:
+                _, dt, reps = O.ref_dequant_timed(2, blk, budget_s, os.path.join(d, "w.gguf"))
+        else:
+            dt, reps = timed(lambda nt=nt: lib.orc_dequant(2, blk.ctypes.data, n, wf.ctypes.data, nt))
         out[f"dequant_cfg1_q4_0_{nt}t"] = {"GB/s": (blk.nbytes + n * 128) / dt / 1e9, "ms": dt * 1e3,
-                                           "threads": nt, "reps": reps}
+                                           "threads": nt, "reps": reps,
+                                           "code": "reference" if nt == 1 and ref else "port"}
     del wf
     K = M = 4096
     T, cols = 512, 8
@@ -396,13 +416,17 @@ def cpu_other_paths(synth, budget_s: float, threads: int):
     bne, bnb = [K, T, 1, 1], [4, 4 * K, 4 * K * T, 4 * K * T]
     dne, dnb = [M, T, 1, 1], [4, 4 * M, 4 * M * T, 4 * M * T]
     for nt in sorted({1, threads}):
-        dt, reps = timed(lambda nt=nt: lib.orc_mul_mat_cols(W.ctypes.data, O.NE(*ane), O.NB(*anb), X.ctypes.data,
-                                                            O.NE(*bne), O.NB(*bnb), Y.ctypes.data, O.NE(*dne),
-                                                            O.NB(*dnb), 0, cols, nt))
+        if nt == 1 and ref:  # the reference's own CPU Device on the first `cols` columns of X
+            _, dt, reps = O.ref_mul_mat_timed(W, K, M, X[: K * cols], cols, budget_s)
+        else:
+            dt, reps = timed(lambda nt=nt: lib.orc_mul_mat_cols(W.ctypes.data, O.NE(*ane), O.NB(*anb),
+                                                                X.ctypes.data, O.NE(*bne), O.NB(*bnb), Y.ctypes.data,
+                                                                O.NE(*dne), O.NB(*dnb), 0, cols, nt))
         fl = 2.0 * K * M * cols
         out[f"mul_mat_cfg3_fwd_{nt}t"] = {"TFLOP/s": fl / dt / 1e12, "ms_slice": dt * 1e3,
                                           "ms_whole_product_extrapolated": dt * 1e3 * T / cols, "threads": nt,
-                                          "reps": reps, "sample": f"{cols} of {T} output columns"}
+                                          "reps": reps, "sample": f"{cols} of {T} output columns",
+                                          "code": "reference" if nt == 1 and ref else "port"}
     return out
 
 

@@ -21,6 +21,8 @@
 //                    CPU buffer, then mul_mat on the CPU Device, repeated and
 //                    timed (the CPU path the fused matvec replaces; bench.py's
 //                    cpu_baseline leg)
+//   ref_dequant_time  -> gguf_tensor_to_f32 alone, repeated and timed
+//   ref_mul_mat_time  -> mul_mat on the CPU Device, repeated and timed
 //   ref_fp16_*    -> core/trc_float.h:23-63
 //   ref_rng_*     -> src/core/trc_rng.cpp:38-68
 #include "traincpp/traincpp.h"
@@ -48,6 +50,47 @@ void put_pod(std::vector<uint8_t>& v, T x) {
 
 void pad32(std::vector<uint8_t>& v) {
     while (v.size() % 32 != 0) v.push_back(0);
+}
+
+// A one-tensor GGUF v3 file (tensor "w", 1-D, n elements of `type` blocks).
+bool write_gguf_w(const char* path, int type, const void* blocks, int64_t n) {
+    const size_t bsz = type_size((Type) type);
+    std::vector<uint8_t> f;
+    put(f, "GGUF", 4);
+    put_pod<uint32_t>(f, 3);
+    put_pod<uint64_t>(f, 1);  // tensors
+    put_pod<uint64_t>(f, 0);  // kvs
+    put_pod<uint64_t>(f, 1);
+    f.push_back('w');
+    put_pod<uint32_t>(f, 1);
+    put_pod<int64_t>(f, n);
+    put_pod<uint32_t>(f, (uint32_t) type);
+    put_pod<uint64_t>(f, 0);
+    pad32(f);
+    put(f, blocks, bsz * (size_t) (n / 32));
+    pad32(f);
+    std::FILE* fp = std::fopen(path, "wb");
+    if (!fp) return false;
+    const bool wrote = std::fwrite(f.data(), 1, f.size(), fp) == f.size();
+    std::fclose(fp);
+    return wrote;
+}
+
+// Runs step() once untimed, then repeatedly for at least budget_s seconds;
+// returns the mean seconds per repetition (negative if a step fails).
+template <typename F>
+double time_steps(F&& step, double budget_s, int* reps_out) {
+    if (!step()) return -5.0;
+    int reps = 0;
+    double el = 0.0;
+    const auto t0 = std::chrono::steady_clock::now();
+    do {
+        if (!step()) return -5.0;
+        ++reps;
+        el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    } while (el < budget_s);
+    *reps_out = reps;
+    return el / reps;
 }
 
 }  // namespace
@@ -113,6 +156,45 @@ int ref_dequant(int type, const void* blocks, int64_t n_blocks, float* out, cons
     return ok ? 0 : -4;
 }
 
+// gguf_tensor_to_f32 of n elements of `type` blocks (a GGUF file written once
+// at tmp_path and opened with its data section loaded) into out, repeated and
+// timed as time_steps does.
+double ref_dequant_time(int type, const void* blocks, int64_t n, float* out, double budget_s, int* reps_out,
+                        const char* tmp_path) {
+    if (type_size((Type) type) == 0 || n <= 0 || n % 32 != 0) return -1.0;
+    if (!write_gguf_w(tmp_path, type, blocks, n)) return -2.0;
+    GgufFile* g = gguf_open(tmp_path, true);
+    std::remove(tmp_path);
+    if (!g) return -3.0;
+    const double dt = time_steps([&]() { return gguf_tensor_to_f32(g, "w", out, n); }, budget_s, reps_out);
+    gguf_close(g);
+    return dt;
+}
+
+// y = mul_mat(A, B) on the reference CPU Device, A = F32 [K, M], B = F32 [K, N]
+// (contiguous), graph built and buffers allocated once; repeated and timed as
+// time_steps does. y gets the [M, N] result.
+double ref_mul_mat_time(const float* a, int64_t K, int64_t M, const float* b, int64_t N, float* y, double budget_s,
+                        int* reps_out) {
+    Device* dev = device_cpu();
+    if (!dev) return -4.0;
+    Context* ctx = context_new(1 << 20);
+    Tensor* ta = new_tensor_2d(ctx, TYPE_F32, K, M);
+    Tensor* tb = new_tensor_2d(ctx, TYPE_F32, K, N);
+    Tensor* r = mul_mat(ctx, ta, tb);
+    Graph* gr = graph_new(ctx);
+    graph_build_forward_expand(ctx, gr, r);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    tensor_set(ta, a, 0, tensor_nbytes(ta));
+    tensor_set(tb, b, 0, tensor_nbytes(tb));
+    const double dt = time_steps([&]() { return dev->graph_compute(gr); }, budget_s, reps_out);
+    if (dt > 0) tensor_get(r, y, 0, tensor_nbytes(r));
+    buffer_free(buf);
+    graph_free(gr);
+    context_free(ctx);
+    return dt;
+}
+
 // The headline workload on the reference's CPU path: W (n = K*M elements of
 // `type` blocks, written once to a GGUF v3 file at tmp_path and opened with its
 // data section loaded) is dequantized by gguf_tensor_to_f32 straight into the
@@ -123,29 +205,8 @@ int ref_dequant(int type, const void* blocks, int64_t n_blocks, float* out, cons
 double ref_headline_time(int type, const void* blocks, int64_t K, int64_t M, const float* x, float* y,
                          double budget_s, int* reps_out, const char* tmp_path) {
     const int64_t n = K * M;
-    const size_t bsz = type_size((Type) type);
-    if (bsz == 0 || n <= 0 || n % 32 != 0) return -1.0;
-    {
-        std::vector<uint8_t> f;
-        put(f, "GGUF", 4);
-        put_pod<uint32_t>(f, 3);
-        put_pod<uint64_t>(f, 1);  // tensors
-        put_pod<uint64_t>(f, 0);  // kvs
-        put_pod<uint64_t>(f, 1);
-        f.push_back('w');
-        put_pod<uint32_t>(f, 1);
-        put_pod<int64_t>(f, n);
-        put_pod<uint32_t>(f, (uint32_t) type);
-        put_pod<uint64_t>(f, 0);
-        pad32(f);
-        put(f, blocks, bsz * (size_t) (n / 32));
-        pad32(f);
-        std::FILE* fp = std::fopen(tmp_path, "wb");
-        if (!fp) return -2.0;
-        const bool wrote = std::fwrite(f.data(), 1, f.size(), fp) == f.size();
-        std::fclose(fp);
-        if (!wrote) return -2.0;
-    }
+    if (type_size((Type) type) == 0 || n <= 0 || n % 32 != 0) return -1.0;
+    if (!write_gguf_w(tmp_path, type, blocks, n)) return -2.0;
     GgufFile* g = gguf_open(tmp_path, true);
     std::remove(tmp_path);
     if (!g) return -3.0;
@@ -162,30 +223,17 @@ double ref_headline_time(int type, const void* blocks, int64_t K, int64_t M, con
     graph_build_forward_expand(ctx, gr, r);
     Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
     tensor_set(xt, x, 0, tensor_nbytes(xt));
-    double result = -5.0;
+    double dt = -6.0;  // the F32 weight has no host-visible buffer
     if (w->data != nullptr) {
-        auto pass = [&]() { return gguf_tensor_to_f32(g, "w", (float*) w->data, n) && dev->graph_compute(gr); };
-        bool ok = pass();  // untimed: touches every page
-        int reps = 0;
-        const auto t0 = std::chrono::steady_clock::now();
-        double el = 0.0;
-        while (ok) {
-            ok = pass();
-            ++reps;
-            el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-            if (el >= budget_s) break;
-        }
-        if (ok) {
-            tensor_get(r, y, 0, tensor_nbytes(r));
-            *reps_out = reps;
-            result = el / reps;
-        }
+        dt = time_steps([&]() { return gguf_tensor_to_f32(g, "w", (float*) w->data, n) && dev->graph_compute(gr); },
+                        budget_s, reps_out);
+        if (dt > 0) tensor_get(r, y, 0, tensor_nbytes(r));
     }
     buffer_free(buf);
     graph_free(gr);
     context_free(ctx);
     gguf_close(g);
-    return result;
+    return dt;
 }
 
 // d = mul_mat(permute(A, pa), permute(B, pb)) on the reference CPU device.

@@ -102,6 +102,10 @@ def ref() -> C.CDLL:
         lib.ref_rng_normal.restype = F
         lib.ref_headline_time.argtypes = [I, P, I64, I64, P, P, C.c_double, C.POINTER(I), C.c_char_p]
         lib.ref_headline_time.restype = C.c_double
+        lib.ref_dequant_time.argtypes = [I, P, I64, P, C.c_double, C.POINTER(I), C.c_char_p]
+        lib.ref_dequant_time.restype = C.c_double
+        lib.ref_mul_mat_time.argtypes = [P, I64, I64, P, I64, P, C.c_double, C.POINTER(I)]
+        lib.ref_mul_mat_time.restype = C.c_double
         _ref = lib
     return _ref
 
@@ -131,6 +135,35 @@ def ref_headline(type_: int, blocks: np.ndarray, x: np.ndarray, K: int, M: int, 
     dt = ref().ref_headline_time(type_, raw.ctypes.data, K, M, xv.ctypes.data, y.ctypes.data, budget_s,
                                  C.byref(reps), tmp_path.encode())
     assert dt > 0, f"ref_headline_time failed ({dt})"
+    return y, dt, reps.value
+
+
+def ref_dequant_timed(type_: int, blocks: np.ndarray, budget_s: float, tmp_path: str) -> tuple[np.ndarray, float, int]:
+    """The reference's gguf_tensor_to_f32 of the blocks, repeated for budget_s
+    seconds after one untimed pass: returns the F32 values, mean seconds per
+    pass and the pass count."""
+    raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+    n = raw.size // oracle().orc_block_bytes(type_) * 32
+    out = np.empty(n, dtype=np.float32)
+    reps = I(0)
+    dt = ref().ref_dequant_time(type_, raw.ctypes.data, n, out.ctypes.data, budget_s, C.byref(reps),
+                                tmp_path.encode())
+    assert dt > 0, f"ref_dequant_time failed ({dt})"
+    return out, dt, reps.value
+
+
+def ref_mul_mat_timed(a: np.ndarray, K: int, M: int, b: np.ndarray, N: int,
+                      budget_s: float) -> tuple[np.ndarray, float, int]:
+    """y = mul_mat(A [K, M], B [K, N]) on the reference CPU Device (contiguous
+    F32), repeated for budget_s seconds after one untimed pass: returns y
+    ([M, N] as N rows of M), mean seconds per pass and the pass count."""
+    av = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    bv = np.ascontiguousarray(b, dtype=np.float32).reshape(-1)
+    assert av.size == K * M and bv.size == K * N
+    y = np.empty(M * N, dtype=np.float32)
+    reps = I(0)
+    dt = ref().ref_mul_mat_time(av.ctypes.data, K, M, bv.ctypes.data, N, y.ctypes.data, budget_s, C.byref(reps))
+    assert dt > 0, f"ref_mul_mat_time failed ({dt})"
     return y, dt, reps.value
 
 

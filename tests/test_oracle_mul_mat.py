@@ -174,3 +174,21 @@ def test_reference_headline_path_matches_oracle(t, tmp_path):
     W = O.dequant(t, raw).reshape(1, 1, M, K)
     want = O.mul_mat(W, x.reshape(1, 1, 1, K)).reshape(-1)
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.skipif(not O.have_ref(), reason="oracle/_ref not built (reference checkout absent)")
+def test_reference_timed_entries_match_oracle(tmp_path):
+    """The timed reference entries bench.py's CPU legs run (gguf_tensor_to_f32
+    alone; mul_mat on the CPU Device) return the oracle's bits."""
+    from traincpp_amd import synth
+    raw = synth.block_bytes(synth.quant_blocks(3, 64, 61))
+    got, dt, reps = O.ref_dequant_timed(3, raw, 0.0, str(tmp_path / "d.gguf"))
+    assert reps >= 1 and dt > 0
+    assert np.array_equal(got.view(np.uint32), O.dequant(3, raw).view(np.uint32))
+    K, M, N = 96, 40, 8
+    a = synth.normal(62, K * M)
+    b = synth.normal(63, K * N)
+    y, dt, reps = O.ref_mul_mat_timed(a, K, M, b, N, 0.0)
+    assert reps >= 1 and dt > 0
+    want = O.mul_mat(a.reshape(1, 1, M, K), b.reshape(1, 1, N, K)).reshape(-1)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
