@@ -121,8 +121,9 @@ class Timer:
             graph, gexec = C.c_void_p(), C.c_void_p()
             try:
                 hip.ok(rt.hipStreamBeginCapture(s, 2), "hipStreamBeginCapture")  # relaxed mode
+                # step i of every replay uses input set i % sets (see rotation_sets)
                 for i in range(steps):
-                    fn(warmup + i, s)
+                    fn(i, s)
                 hip.ok(rt.hipStreamEndCapture(s, C.byref(graph)), "hipStreamEndCapture")
                 hip.ok(rt.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0), "hipGraphInstantiate")
                 exec_ = gexec.value
@@ -146,7 +147,7 @@ class Timer:
                 hip.ok(rt.hipGraphLaunch(exec_, s), "hipGraphLaunch")
             else:
                 for i in range(steps):
-                    fn(warmup + i, s)
+                    fn(i, s)
             hip.ok(rt.hipEventRecord(self.e1, s), "record")
             hip.ok(rt.hipEventSynchronize(self.e1), "sync")
             hip.ok(rt.hipDeviceSynchronize(), "sync")
@@ -163,11 +164,27 @@ def rotation_count(bytes_per_set: int, floor: int = 3, target: int = 512 << 20) 
     return max(floor, -(-target // max(bytes_per_set, 1)) + 1)
 
 
+def rotation_sets(bytes_per_set: int, steps: int) -> int:
+    """Input sets for a timed graph of `steps` launches in which step i reads set
+    i % sets. The smallest divisor of `steps` that is at least rotation_count(), so
+    that a replay ends on the last set and the next replay starts on set 0: between
+    two reads of one set, every other set is read, more than 512 MB (twice the
+    Infinity Cache), across replay boundaries too. With fewer steps than that
+    count, every step of a replay reads its own set."""
+    need = rotation_count(bytes_per_set)
+    # (with fewer steps than `need`, a replay reads `steps` different sets and the
+    # next replay reads them again)
+    for d in range(need, steps + 1):
+        if steps % d == 0:
+            return d
+    return need
+
+
 def qmatvec_case(H, synth, timer, t, K, M, N, steps, warmup, cfg=2):
     blk = synth.block_bytes(synth.quant_blocks(t, K * M // 32, synth.config_seed(cfg, t)))
     x = synth.normal(synth.config_seed(cfg, 100 + N), K * N)
     alg_bytes = blk.nbytes + x.nbytes + M * N * 4
-    sets = rotation_count(alg_bytes)
+    sets = rotation_sets(alg_bytes, steps)
     ws = [H.DeviceBuffer(blk.nbytes).upload(blk) for _ in range(sets)]
     xs = [H.DeviceBuffer(x.nbytes).upload(x) for _ in range(sets)]
     ys = [H.DeviceBuffer(M * N * 4) for _ in range(sets)]
@@ -191,7 +208,7 @@ def qmatvec_case(H, synth, timer, t, K, M, N, steps, warmup, cfg=2):
 def dequant_case(H, synth, timer, t, n_blocks, steps, warmup):
     blk = synth.block_bytes(synth.quant_blocks(t, n_blocks, synth.config_seed(1, t)))
     alg_bytes = blk.nbytes + n_blocks * 32 * 4
-    sets = rotation_count(alg_bytes)
+    sets = rotation_sets(alg_bytes, steps)
     srcs = [H.DeviceBuffer(blk.nbytes).upload(blk) for _ in range(sets)]
     dsts = [H.DeviceBuffer(n_blocks * 128) for _ in range(sets)]
 
@@ -264,6 +281,44 @@ def mul_mat_config4(H, synth, timer, steps, warmup):
         x.free()
     return {"ms": ms, "TFLOP/s": fl / (ms * 1e-3) / 1e12, "frac_mfma": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFS,
             "timing": mode}
+
+
+def mul_mat_config0(H, synth, timer, N, steps, warmup):
+    """Configuration 0's product after the GGUF warm start: W F32 [4096, 4096] (the
+    GPU dequant of the Q8_0 blocks) times X F32 [4096, N] through
+    trc_hip_mul_mat_f32. HBM-bound: algorithmic bytes = W + X + Y."""
+    K = M = 4096
+    n = K * M // 32
+    raw = synth.block_bytes(synth.quant_blocks(H.TYPE_Q8_0, n, synth.config_seed(0, 8)))
+    x = synth.normal(synth.config_seed(0, 100 + N), K * N)
+    alg_bytes = K * M * 4 + x.nbytes + M * N * 4
+    sets = rotation_sets(alg_bytes, steps)
+    qd = H.DeviceBuffer(raw.nbytes).upload(raw)
+    ws = [H.DeviceBuffer(K * M * 4) for _ in range(sets)]
+    for w in ws:
+        H.dequant(H.TYPE_Q8_0, qd.ptr, n, w.ptr)
+    H.sync()
+    qd.free()
+    xs = [H.DeviceBuffer(x.nbytes).upload(x) for _ in range(sets)]
+    ys = [H.DeviceBuffer(M * N * 4) for _ in range(sets)]
+    ts = [(H.tensor(w.ptr, [K, M, 1, 1], H.contiguous_nb([K, M, 1, 1])),
+           H.tensor(xb.ptr, [K, N, 1, 1], H.contiguous_nb([K, N, 1, 1])),
+           H.tensor(yb.ptr, [M, N, 1, 1], H.contiguous_nb([M, N, 1, 1]))) for w, xb, yb in zip(ws, xs, ys)]
+
+    def step(i, s):
+        a, b, d = ts[i % sets]
+        H.mul_mat_f32(a, b, d, s)
+
+    ms, mode = timer.run(step, steps, warmup)
+    reps = list(timer.last_replays)
+    for b in ws + xs + ys:
+        b.free()
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    fl = 2.0 * K * M * N
+    return {"us": ms * 1e3, "bytes": alg_bytes, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS,
+            "TFLOP/s": fl / (ms * 1e-3) / 1e12, "sets": sets, "timing": mode,
+            "replays_us": [round(r * 1e3, 3) for r in reps],
+            "kernel": "k_mm_skinny (train.cpp_amd/csrc/hip/mul_mat.hip)"}
 
 
 # ---------------------------------------------------------------- CPU baseline (reference path, oracle/)
@@ -517,10 +572,11 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time a 256 MiB device copy (reference for the traffic counters)")
-    ap.add_argument("--only", choices=["dequant", "mul_mat", "qmm", "cfg0", "qmm_sweep"],
+    ap.add_argument("--only", choices=["dequant", "mul_mat", "qmm", "cfg0", "qmm_sweep", "mm0", "mm0_sweep"],
                     help="only time one hot path and print its figures (for counter runs): dequant = the five "
                          "formats on configuration 1, mul_mat = configurations 3 and 4, qmm = Q4_0 N=16 on "
-                         "configuration 2, qmm_sweep = Q4_0 on configuration 2 for N from 1 to 64")
+                         "configuration 2, qmm_sweep = Q4_0 on configuration 2 for N from 1 to 64, mm0 = "
+                         "configuration 0's F32 product (8 columns), mm0_sweep = the same for N from 1 to 64")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; multi-GPU runs are not part of this "
@@ -547,6 +603,13 @@ def main():
             part["cfg4"] = mul_mat_config4(H, synth, timer, args.steps, args.warmup)
         elif args.only == "qmm":
             part["q4_0 N=16"], _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 16, args.steps, args.warmup)
+        elif args.only == "mm0":
+            part["N=8"] = mul_mat_config0(H, synth, timer, 8, args.steps, args.warmup)
+        elif args.only == "mm0_sweep":
+            for n in (8, 1, 2, 3, 4, 16, 24, 32, 48, 64):
+                r = mul_mat_config0(H, synth, timer, n, args.steps, args.warmup)
+                part[f"N={n}"] = {"us": round(r["us"], 2), "frac_hbm": round(r["frac_hbm"], 4),
+                                  "TFLOP/s": round(r["TFLOP/s"], 2), "replays_us": r["replays_us"]}
         elif args.only == "cfg0":
             part["q8_0 4096x4096 N=8"], _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q8_0, 4096, 4096, 8, args.steps,
                                                            args.warmup, cfg=0)
@@ -587,6 +650,9 @@ def main():
         # configuration 0's product: Q8_0 W[4096,4096] times x with 8 columns, fused
         r, _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q8_0, 4096, 4096, 8, s, w, cfg=0)
         extra["qmatvec_cfg0_q8_0_4096x4096_n8"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+        # configuration 0 as the reference runs it: the F32 weight of the warm start times 8 columns
+        r = mul_mat_config0(H, synth, timer, 8, s, w)
+        extra["mul_mat_cfg0_f32_4096x4096x8"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
         extra["dequant_4096x11008"] = {}
         for name, t in H.QUANT_TYPES.items():
             r = dequant_case(H, synth, timer, t, 4096 * 11008 // 32, s, w)

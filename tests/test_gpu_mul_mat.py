@@ -250,3 +250,70 @@ def test_shape_errors_are_rejected(hip):
     assert e.value.code == H.E_SHAPE
     for t in (buf, b3):
         t.free()
+
+
+# ---------------------------------------------------------------- few columns (N <= 64)
+
+@pytest.fixture(scope="module")
+def cfg0_w():
+    """Configuration 0's weight: the Q8_0 blocks of a 4096 x 4096 tensor as the GGUF
+    warm start turns them into F32 (src/io/trc_gguf.cpp:1082-1088), here by the oracle."""
+    n = 4096 * 4096 // 32
+    raw = synth.block_bytes(synth.quant_blocks(H.TYPE_Q8_0, n, synth.config_seed(0, 8)))
+    return O.dequant(H.TYPE_Q8_0, raw, threads=8).reshape(1, 1, 4096, 4096)
+
+
+@pytest.mark.parametrize("N", [1, 2, 3, 8, 16, 32, 64])
+@pytest.mark.parametrize("layout", ["contiguous", "transposed"])
+def test_config0_f32_few_columns(hip, cfg0_w, N, layout):
+    """mul_mat(W F32 [4096, 4096], X [4096, N]) at configuration 0's size, every dst
+    element against the oracle: X k-contiguous, or X = transpose(base[N, 4096])
+    (k strided, the layout of a transposed activation view)."""
+    announce(f"mul_mat cfg0 F32 N={N} {layout}")
+    X = synth.normal(synth.config_seed(0, 100 + N), 4096 * N)
+    if layout == "contiguous":
+        got, want = run_views(cfg0_w, lambda x: x, X.reshape(1, 1, N, 4096), lambda x: x)
+    else:
+        got, want = run_views(cfg0_w, lambda x: x, X.reshape(1, 1, 4096, N), t01)
+    assert got.shape == (1, 1, N, 4096)
+    assert O.row_l2_error(got, want) <= TOL
+
+
+def test_config0_f32_deterministic(hip, cfg0_w):
+    """The waves' partial sums meet in a fixed order: two runs give the same bits."""
+    announce("mul_mat cfg0 F32 N=8 twice")
+    X = synth.normal(synth.config_seed(0, 108), 4096 * 8).reshape(1, 1, 8, 4096)
+    a, _ = run_views(cfg0_w, lambda x: x, X, lambda x: x)
+    b, _ = run_views(cfg0_w, lambda x: x, X, lambda x: x)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [
+    # K, M, N, b2, b3, a2, a3: ragged row blocks, K not a multiple of the 32-wide chunk,
+    # fewer chunks than waves, every column-group count, broadcast planes
+    (4, 1, 1, 1, 1, 1, 1), (36, 17, 5, 1, 1, 1, 1), (100, 33, 16, 1, 1, 1, 1), (512, 70, 17, 1, 1, 1, 1),
+    (1028, 250, 33, 1, 1, 1, 1), (2048, 300, 48, 1, 1, 1, 1), (260, 129, 64, 1, 1, 1, 1),
+    (128, 64, 8, 4, 2, 2, 1), (96, 48, 24, 6, 1, 3, 1), (64, 40, 64, 2, 2, 1, 2),
+])
+@pytest.mark.parametrize("layout", ["kk", "kt", "kgen", "kmis"])
+def test_few_columns_shapes(hip, shape, layout):
+    """The few-column path (N <= 64, W k-contiguous) on ragged shapes and planes, with
+    X k-contiguous (kk), transposed (kt), every other element (kgen) or 4 bytes off
+    16-byte alignment (kmis: read element by element)."""
+    K, M, N, b2, b3, a2, a3 = shape
+    rng = np.random.default_rng(K * 11 + M * 5 + N)
+    announce(f"mul_mat few columns {shape} {layout}")
+    A = rng.standard_normal((a3, a2, M, K)).astype(np.float32)
+    if layout == "kk":
+        B = rng.standard_normal((b3 * a3, b2 * a2, N, K)).astype(np.float32)
+        got, want = run_views(A, lambda x: x, B, lambda x: x)
+    elif layout == "kt":
+        B = rng.standard_normal((b3 * a3, b2 * a2, K, N)).astype(np.float32)
+        got, want = run_views(A, lambda x: x, B, t01)
+    elif layout == "kgen":
+        B = rng.standard_normal((b3 * a3, b2 * a2, N, 2 * K)).astype(np.float32)
+        got, want = run_views(A, lambda x: x, B, lambda x: x[..., ::2])
+    else:
+        B = rng.standard_normal((b3 * a3, b2 * a2, N, K + 1)).astype(np.float32)
+        got, want = run_views(A, lambda x: x, B, lambda x: x[..., 1:])
+    assert O.row_l2_error(got, want) <= TOL

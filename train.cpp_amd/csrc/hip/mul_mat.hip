@@ -35,6 +35,8 @@
 //     two: 8-wave workgroups (64x32 per wave) each sum half of K for one tile,
 //     into a dst cleared beforehand, with float atomic adds. 0 + a + b rounds
 //     the same in either order, so results stay deterministic.
+//   - Up to 64 columns against a k-contiguous src0 (decode-sized batches) take
+//     k_mm_skinny below instead: one pass over src0 on every CU.
 #include "common.h"
 
 namespace trc_hip {
@@ -261,6 +263,184 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
     }
 }
 
+// ---------------------------------------------------------------- few columns
+//
+// dst = W . X with N <= 64 columns and W k-contiguous (the weight of a Linear
+// layer run at decode batch, e.g. the F32 weight a GGUF warm start produces,
+// src/io/trc_gguf.cpp:1082-1088, times 8 activation columns): W is read from
+// HBM once, so the product is bound by W's bytes, not by MFMA work.
+//   - One workgroup per 16 rows of W (one row block of one plane) and all of K;
+//     its SK_WAVES waves take the 32-wide k chunks in turn (chunk c to wave
+//     c % SK_WAVES), so every wave streams its own part of the 16 rows. Row
+//     block rb starts at chunk 37 rb (mod the chunk count), so the workgroups
+//     in flight read different offsets of their rows (rows 16 KiB apart would
+//     otherwise all start on the same offset: 4 % faster on configuration 0).
+//   - Lane l reads row l % 16 of the block at k = 32c + 4g .. +3 and
+//     32c + 16 + 4g .. +3 (g = l / 16): two float4 loads, 64 contiguous bytes
+//     per row and instruction. It reads X column 16t + l % 16 at the same k.
+//   - v_mfma_f32_16x16x4_f32 with X as the A operand (MFMA row = column j of X)
+//     and W as the B operand (MFMA column = row i of W); A and B take the same
+//     k from the same lane, so any k order within a chunk gives the same dot.
+//     Accumulator register v of lane l then holds dst row i = l % 16, column
+//     j = 16t + 4 (l / 16) + v.
+//   - Loads go through buffer resources (16 rows of W, one plane of X): an
+//     element outside the operands gets an offset past its resource, which the
+//     hardware reads as 0. No branch or select waits on a load, so AHEAD chunks
+//     per wave stay in flight ahead of the MFMAs (the loads for chunk n + AHEAD
+//     are issued once chunk n's registers are consumed).
+//   - The waves' partial sums meet in LDS and are added in wave order
+//     (0 + w0 + w1 + ...), so results do not depend on timing.
+
+struct SkArgs {
+    const uint8_t* a;
+    const uint8_t* b;
+    uint8_t* d;
+    int64_t K, M, N;
+    int64_t a_nb1, a_nb2, a_nb3, a_ne2, a_ne3;
+    int64_t b_nb0, b_nb1, b_nb2, b_nb3, b_ne2;
+    int64_t d_nb0, d_nb1, d_nb2, d_nb3;
+    int64_t row_blocks;  // ceil(M / 16)
+    int64_t x_span;      // bytes from one X plane's first element to past its last
+    int chunks;          // ceil(K / 32)
+};
+
+constexpr int SK_WAVES = 16;
+constexpr int SK_MAX_N = 64;
+constexpr uint32_t SK_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
+constexpr uint32_t SK_OUT = 0x80000000u;         // an offset past every resource: the load returns 0
+
+// One chunk's operands in registers: W (two float4) and X (two float4 per
+// 16-column group).
+template <int NT>
+struct SkChunk {
+    f4 w0, w1;
+    f4 x0[NT], x1[NT];
+};
+
+// Loads this wave's n-th chunk (chunk index wave + SK_WAVES * n, rotated by rot).
+template <int NT, int BMODE>
+__device__ __forceinline__ void sk_load(SkChunk<NT>& c, __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rx,
+                                        uint32_t wrow_off, const SkArgs& p, int wave, int n, int mine, int g, int r,
+                                        int rot) {
+    const bool chunk_ok = n < mine;
+    int chunk = wave + SK_WAVES * n + rot;
+    chunk = chunk >= p.chunks ? chunk - p.chunks : chunk;
+    const int k0 = chunk * 32 + 4 * g;
+    const int k1 = k0 + 16;
+    // K % 4 == 0 on this path: a float4 is wholly inside K or wholly past it
+    const bool ok0 = chunk_ok && k0 < p.K, ok1 = chunk_ok && k1 < p.K;
+    // rows past M lie past rw's range by construction
+    c.w0 = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok0 ? wrow_off + 4u * k0 : SK_OUT, 0, 0));
+    c.w1 = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok1 ? wrow_off + 4u * k1 : SK_OUT, 0, 0));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int j = 16 * t + r;
+        const bool c0 = ok0 && j < p.N, c1 = ok1 && j < p.N;
+        const uint32_t col = (uint32_t) j * (uint32_t) p.b_nb1;
+        if constexpr (BMODE == K_CONTIG) {
+            c.x0[t] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, c0 ? col + 4u * k0 : SK_OUT, 0, 0));
+            c.x1[t] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, c1 ? col + 4u * k1 : SK_OUT, 0, 0));
+        } else {
+            const uint32_t nb0 = (uint32_t) p.b_nb0;
+            const uint32_t o0 = c0 ? col + nb0 * (uint32_t) k0 : SK_OUT;
+            const uint32_t o1 = c1 ? col + nb0 * (uint32_t) k1 : SK_OUT;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                c.x0[t][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, c0 ? o0 + nb0 * e : SK_OUT, 0, 0));
+                c.x1[t][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, c1 ? o1 + nb0 * e : SK_OUT, 0, 0));
+            }
+        }
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void sk_mfma(const SkChunk<NT>& c, f4 (&acc)[NT]) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(c.x0[t][s], c.w0[s], acc[t], 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(c.x1[t][s], c.w1[s], acc[t], 0, 0, 0);
+    }
+}
+
+template <int NT, int AHEAD, int BMODE>
+__global__ __launch_bounds__(SK_WAVES * 64) void k_mm_skinny(SkArgs p) {
+    __shared__ float red[SK_WAVES * NT * 4 * 64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+
+    const int64_t rb = blockIdx.x % p.row_blocks;
+    const int64_t plane = blockIdx.x / p.row_blocks;
+    const int64_t i2 = plane % p.b_ne2;
+    const int64_t i3 = plane / p.b_ne2;
+    const uint8_t* aplane = p.a + (i2 % p.a_ne2) * p.a_nb2 + (i3 % p.a_ne3) * p.a_nb3;
+    const uint8_t* bplane = p.b + i2 * p.b_nb2 + i3 * p.b_nb3;
+
+    // W rows rb*16 .. of this plane up to the last valid byte of the last valid row;
+    // X of this plane up to its last element (spans checked below 2^31 on the host)
+    const int64_t rows = p.M - rb * 16 < 16 ? p.M - rb * 16 : 16;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void*) (aplane + rb * 16 * p.a_nb1), (short) 0, (int) ((rows - 1) * p.a_nb1 + p.K * 4), SK_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*) bplane, (short) 0, (int) p.x_span, SK_RSRC_WORD3);
+    const uint32_t wrow_off = (uint32_t) r * (uint32_t) p.a_nb1;
+
+    f4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = (f4){0.f, 0.f, 0.f, 0.f};
+
+    // this wave's chunks: wave, wave + SK_WAVES, ... (mine of them). The last
+    // batch of AHEAD chunks runs after the loop, with no loads behind it; chunks
+    // past `mine` in it were loaded as zeros.
+    const int mine = wave < p.chunks ? (p.chunks - 1 - wave) / SK_WAVES + 1 : 0;
+    const int rot = (int) ((rb * 37) % p.chunks);
+    SkChunk<NT> buf[AHEAD];
+#pragma unroll
+    for (int u = 0; u < AHEAD; ++u) sk_load<NT, BMODE>(buf[u], rw, rx, wrow_off, p, wave, u, mine, g, r, rot);
+    int n0 = 0;
+    for (; n0 + AHEAD < mine; n0 += AHEAD) {
+#pragma unroll
+        for (int u = 0; u < AHEAD; ++u) {
+            sk_mfma<NT>(buf[u], acc);
+            sk_load<NT, BMODE>(buf[u], rw, rx, wrow_off, p, wave, n0 + AHEAD + u, mine, g, r, rot);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < AHEAD; ++u) sk_mfma<NT>(buf[u], acc);
+
+    // partial sums of every wave, then the sum over waves in wave order
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[(wave * NT * 4 + t * 4 + v) * 64 + lane] = acc[t][v];
+    __syncthreads();
+    for (int e = threadIdx.x; e < NT * 4 * 64; e += SK_WAVES * 64) {
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < SK_WAVES; ++w) s += red[w * NT * 4 * 64 + e];
+        const int el = e & 63, tv = e >> 6;  // tv = 4t + v
+        const int64_t j = 16 * (tv >> 2) + 4 * (el >> 4) + (tv & 3);
+        const int64_t di = rb * 16 + (el & 15);
+        if (di < p.M && j < p.N) *(float*) (p.d + i2 * p.d_nb2 + i3 * p.d_nb3 + di * p.d_nb0 + j * p.d_nb1) = s;
+    }
+}
+
+template <int NT, int AHEAD>
+int launch_skinny_nt(SkArgs& p, int bmode, int64_t planes, hipStream_t stream) {
+    const int64_t grid = p.row_blocks * planes;
+    if (grid > 0x7FFFFFFF) return fail(TRC_HIP_E_SHAPE, "mul_mat: %lld workgroups exceed one launch", (long long) grid);
+    if (bmode == K_CONTIG) {
+        hipLaunchKernelGGL((k_mm_skinny<NT, AHEAD, K_CONTIG>), dim3((unsigned) grid), dim3(SK_WAVES * 64), 0, stream, p);
+    } else {
+        // element-by-element X loads hold more addresses: half as many chunks ahead
+        constexpr int GA = AHEAD > 1 ? AHEAD / 2 : 1;
+        hipLaunchKernelGGL((k_mm_skinny<NT, GA, GENERIC>), dim3((unsigned) grid), dim3(SK_WAVES * 64), 0, stream, p);
+    }
+    return check_launch("mul_mat_f32 (few columns)");
+}
+
 int pick_mode(const trc_hip_tensor& t, int64_t rows) {
     const uintptr_t base = (uintptr_t) t.data;
     if (t.nb[0] == 4 && t.ne[0] % 4 == 0 && t.nb[1] % 16 == 0 && t.nb[2] % 16 == 0 && t.nb[3] % 16 == 0 &&
@@ -321,6 +501,29 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
     const int am = pick_mode(a, p.M);
     const int bm = pick_mode(b, p.N);
     const int64_t planes = b.ne[2] * b.ne[3];
+
+    // Up to 64 columns against a k-contiguous W: one pass over W on every CU.
+    // Its loads address 16 rows of W and one plane of X through 32-bit offsets.
+    const int64_t x_span = (p.N - 1) * p.b_nb1 + (p.K - 1) * p.b_nb0 + 4;
+    if (p.N <= SK_MAX_N && am == K_CONTIG && 16 * p.a_nb1 + 4 * p.K < ((int64_t) 1 << 31) &&
+        x_span < ((int64_t) 1 << 31) && p.b_nb0 < ((int64_t) 1 << 31) && p.b_nb1 < ((int64_t) 1 << 31) &&
+        (p.K + 31) / 32 < ((int64_t) 1 << 26)) {
+        SkArgs s;
+        s.a = p.a; s.b = p.b; s.d = p.d;
+        s.K = p.K; s.M = p.M; s.N = p.N;
+        s.a_nb1 = p.a_nb1; s.a_nb2 = p.a_nb2; s.a_nb3 = p.a_nb3; s.a_ne2 = p.a_ne2; s.a_ne3 = p.a_ne3;
+        s.b_nb0 = p.b_nb0; s.b_nb1 = p.b_nb1; s.b_nb2 = p.b_nb2; s.b_nb3 = p.b_nb3; s.b_ne2 = p.b_ne2;
+        s.d_nb0 = p.d_nb0; s.d_nb1 = p.d_nb1; s.d_nb2 = p.d_nb2; s.d_nb3 = p.d_nb3;
+        s.row_blocks = (p.M + 15) / 16;
+        s.x_span = x_span;
+        s.chunks = (int) ((p.K + 31) / 32);
+        // K_CONTIG operands are 16-byte aligned with K % 4 == 0; anything else is read element by element
+        const int sbm = bm == K_CONTIG ? K_CONTIG : GENERIC;
+        if (p.N <= 16) return launch_skinny_nt<1, 4>(s, sbm, planes, stream);
+        if (p.N <= 32) return launch_skinny_nt<2, 2>(s, sbm, planes, stream);
+        if (p.N <= 48) return launch_skinny_nt<3, 2>(s, sbm, planes, stream);
+        return launch_skinny_nt<4, 1>(s, sbm, planes, stream);
+    }
 
     // Large tiles when they still give every CU at least two workgroups. With
     // between half and two tiles per CU and a long K, large tiles with K in two
