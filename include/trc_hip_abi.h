@@ -154,21 +154,36 @@ int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b,
  *       x and nb1_x 16-byte aligned)
  *   y : F32, ne = [M, N]; column n starts at y + n*nb1_y bytes (y[m] contiguous;
  *       4-byte aligned)
- * with K % 32 == 0 and 1 <= N <= TRC_HIP_QMATVEC_MAX_N. y must not share a byte
- * with W or x (TRC_HIP_E_SHAPE otherwise). The blocks are decoded in registers
+ * with K % 32 == 0 and 1 <= N <= TRC_HIP_QMATVEC_MAX_N. The address span y covers
+ * (from its first to its last element) must not intersect the spans of W and x,
+ * even where no byte is shared, as with interleaved columns (TRC_HIP_E_SHAPE
+ * otherwise). The blocks are decoded in registers
  * and never written out as F32. There is no counterpart in the reference: its
  * CPU path rejects quantized mul_mat (src/ops/trc_ops.cpp:368) and the
  * equivalent result is gguf_tensor_to_f32 followed by F32 mul_mat.
- * Streams: calls on different streams may overlap. For 2 <= N <= 32 (and the
- * 32-column slices of wider N) x is converted into a device workspace of about
- * 8.3 MiB that belongs to the (device, stream) pair: the first such call on a
- * stream allocates it (hipMalloc; make that call before capturing the stream
- * into a graph in global capture mode) and it is kept until the process ends.
- * A captured graph keeps using the workspace of the stream it was captured on,
- * so do not replay it concurrently with other work on that stream's workspace. */
+ * Streams: calls on different streams may overlap. Shapes that run the x
+ * pre-pass (most of 2 <= N <= 32 and the 32-column slices of wider N) convert x
+ * into a device workspace of about 8.3 MiB that belongs to the (device, stream)
+ * pair: the first such call on a stream allocates it (hipMalloc; make that call
+ * before capturing the stream into a graph in global capture mode). Each device
+ * keeps at most 8 such workspaces; the first call on a ninth stream waits for
+ * the device to go idle (hipDeviceSynchronize) and takes over the least recently
+ * used one. Call trc_hip_qmatvec_release_stream before destroying a stream to
+ * free its workspace. A captured graph keeps using the workspace of the stream
+ * it was captured on, so do not replay it concurrently with other work on that
+ * stream's workspace, and do not release that stream while the graph is live. */
 int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w,
                     const float* x, int64_t N, size_t nb1_x,
                     float* y, size_t nb1_y, void* stream);
+
+/* Frees the x workspace trc_hip_qmatvec keeps for `stream` on the current
+ * device, after waiting for the stream's queued work (hipStreamSynchronize).
+ * Call it before hipStreamDestroy; a later call on the stream allocates a new
+ * workspace. hipStreamPerThread is keyed by the calling thread. Returns
+ * TRC_HIP_OK when the stream has no workspace. No counterpart in the reference:
+ * it bounds the memory of trc_hip_qmatvec's per-stream workspaces, like the
+ * ownership rule of Buffer (include/traincpp/trc_backend.h:33-88). */
+int trc_hip_qmatvec_release_stream(void* stream);
 
 /* trc_hip_qmatvec without any allocation, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses

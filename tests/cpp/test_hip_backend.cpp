@@ -535,6 +535,59 @@ void test_quantized_graph(Device* dev, const std::string& dir) {
     }
 }
 
+// mul_mat(quant W, x) where x is not 16-byte aligned (a view 4 bytes into a
+// wider tensor, so its data and its column stride are only 4-byte aligned): the
+// fused kernels need 16-byte aligned columns, so the device dequantizes W into
+// its scratch and runs the F32 product on the view as it lies.
+void test_quantized_misaligned_x(Device* dev, const std::string& dir) {
+    std::printf("quantized mul_mat with a misaligned activation view\n");
+    const Type types[] = {TYPE_Q4_0, TYPE_Q4_1, TYPE_Q5_0, TYPE_Q5_1, TYPE_Q8_0};
+    const int64_t K = 256, M = 200;
+    for (Type qt : types) {
+        for (int64_t N : {1, 8, 40}) {
+            const std::vector<uint8_t> blocks = quant_blocks(qt, K * M / 32, 177 + (uint64_t) qt);
+            const std::string path = dir + "/qm_" + type_name(qt) + ".gguf";
+            EXPECT(write_gguf(path, "w", qt, {K, M}, blocks, false));
+            GgufFile* f = gguf_open(path.c_str(), true);
+            EXPECT(f != nullptr);
+            if (!f) continue;
+            Context* ctx = context_new(1 << 20);
+            Tensor* wq = gguf_new_tensor(ctx, f, "w", qt);
+            Tensor* xw = new_tensor_2d(ctx, TYPE_F32, K + 1, N);  // columns of K + 1 floats
+            Tensor* xv = view_2d(ctx, xw, K, N, 4);              // skip each column's first float
+            Tensor* y = mul_mat(ctx, wq, xv);
+            Graph* g = graph_new(ctx);
+            graph_build_forward_expand(ctx, g, y);
+            EXPECT(graph_first_unsupported(g, dev) == nullptr);
+            Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+            EXPECT(gguf_load_tensor(f, "w", wq));
+            const std::vector<float> XW = normal((size_t) ((K + 1) * N), 19 + (uint64_t) N);
+            tensor_set(xw, XW.data(), 0, XW.size() * 4);
+            EXPECT(dev->graph_compute(g));
+            std::vector<float> gy((size_t) (M * N));
+            tensor_get(y, gy.data(), 0, gy.size() * 4);
+            // oracle: dequantize, then mul_mat on the same (strided) view
+            const std::vector<float> want_w = oracle_dequant(qt, blocks);
+            const int64_t ane[4] = {K, M, 1, 1};
+            const size_t anb[4] = {4, (size_t) (4 * K), (size_t) (4 * K * M), (size_t) (4 * K * M)};
+            const int64_t dne[4] = {M, N, 1, 1};
+            const size_t dnb[4] = {4, (size_t) (4 * M), (size_t) (4 * M * N), (size_t) (4 * M * N)};
+            std::vector<float> want((size_t) (M * N));
+            EXPECT(orc_mul_mat(want_w.data(), ane, anb, XW.data() + 1, xv->ne, xv->nb, want.data(), dne, dnb, 8) == 0);
+            const bool misaligned = ((xv->data_offset - xw->data_offset) % 16) != 0 && xv->nb[1] % 16 != 0;
+            const double e = row_l2_error(gy, want, M);
+            EXPECT(misaligned && e <= 1e-4);
+            std::printf("    [%s] %-5s N=%-3lld view offset 4, nb1 %zu: mul_mat err %.2e\n",
+                        (misaligned && e <= 1e-4) ? " OK " : "FAIL", type_name(qt), (long long) N, xv->nb[1], e);
+            buffer_free(buf);
+            graph_free(g);
+            context_free(ctx);
+            gguf_close(f);
+            std::remove(path.c_str());
+        }
+    }
+}
+
 void test_fill_and_unsupported(Device* dev) {
     std::printf("fill_tensors / supports_op\n");
     Context* ctx = context_new(1 << 16);
@@ -948,6 +1001,7 @@ int main(int argc, char** argv) {
         test_autograd_linear_bias(dev);
         test_gguf_config0(dev, dir);
         test_quantized_graph(dev, dir);
+        test_quantized_misaligned_x(dev, dir);
         test_fill_and_unsupported(dev);
     }
     std::printf("%s: %d failure(s)\n", g_failures == 0 ? "PASS" : "FAIL", g_failures);

@@ -52,24 +52,52 @@ def gpu_mul_mat(a_dev: Dev, a_view, b_dev: Dev, b_view) -> np.ndarray:
     return res
 
 
+_RT = None
+
+
+def runtime() -> C.CDLL:
+    """The HIP runtime the library links (for streams, graphs and memory queries)."""
+    global _RT
+    if _RT is None:
+        rt = C.CDLL("libamdhip64.so")
+        V, PV = C.c_void_p, C.POINTER(C.c_void_p)
+        for name, args in {
+            "hipStreamCreate": [PV], "hipStreamDestroy": [V], "hipStreamBeginCapture": [V, C.c_int],
+            "hipStreamEndCapture": [V, PV], "hipGraphInstantiate": [PV, V, V, V, C.c_size_t],
+            "hipGraphLaunch": [V, V], "hipGraphExecDestroy": [V], "hipGraphDestroy": [V],
+            "hipMemGetInfo": [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)], "hipDeviceSynchronize": [],
+            "hipGetLastError": [],
+        }.items():
+            fn = getattr(rt, name)
+            fn.argtypes = args
+            fn.restype = C.c_int
+        _RT = rt
+    return _RT
+
+
+def mem_free() -> int:
+    """Free device memory (hipMemGetInfo) after the device has gone idle."""
+    rt = runtime()
+    assert rt.hipDeviceSynchronize() == 0
+    free, total = C.c_size_t(), C.c_size_t()
+    assert rt.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
 class Stream:
     """A HIP stream of the runtime the library uses (hipStreamCreate/Destroy),
     passed to the C ABI as its opaque handle."""
 
-    _rt = None
-
     def __init__(self):
-        if Stream._rt is None:
-            rt = C.CDLL("libamdhip64.so")
-            rt.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
-            rt.hipStreamDestroy.argtypes = [C.c_void_p]
-            Stream._rt = rt
         h = C.c_void_p()
-        assert Stream._rt.hipStreamCreate(C.byref(h)) == 0
+        assert runtime().hipStreamCreate(C.byref(h)) == 0
         self.handle = h.value
 
     def close(self):
+        """Frees the stream's qmatvec workspace (after its work), then destroys it,
+        in the order include/trc_hip_abi.h asks of callers."""
         if self.handle:
+            H.qmatvec_release_stream(self.handle)
             H.sync(self.handle)
-            assert Stream._rt.hipStreamDestroy(C.c_void_p(self.handle)) == 0
+            assert runtime().hipStreamDestroy(C.c_void_p(self.handle)) == 0
             self.handle = None

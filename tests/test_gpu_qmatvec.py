@@ -9,7 +9,7 @@ import pytest
 
 import oracle_lib as O
 from conftest import announce
-from gpu_util import Dev, Stream, empty
+from gpu_util import Dev, Stream, empty, mem_free
 from test_oracle_dequant import TYPES
 from traincpp_amd import hip as H
 from traincpp_amd import synth
@@ -378,6 +378,50 @@ def test_two_streams_do_not_share_x(hip):
             d.free()
     for s in streams:
         s.close()
+
+
+def test_stream_workspaces_are_released_and_bounded(hip):
+    """The 16-column path converts x into a workspace per stream. 64 streams are
+    created and destroyed, each with one call and trc_hip_qmatvec_release_stream
+    before hipStreamDestroy: free device memory comes back to within 1 MiB of its
+    start. Then 12 streams stay alive without a release: the device keeps at most
+    8 workspaces, so memory grows by at most 8 of them. Every result equals the
+    null stream's bit for bit."""
+    t = TYPES["q4_0"]
+    K, M, N = 4096, 2048, 16
+    raw = synth.block_bytes(synth.quant_blocks(t, K * M // 32, 930))
+    X = synth.normal(931, K * N).reshape(1, 1, N, K)
+    dw, dx, dy = Dev(raw), Dev(X), empty((1, 1, N, M))
+
+    def call(stream):
+        H.qmatvec(t, dw.ptr, K, M, (K // 32) * 18, dx.ptr, N, K * 4, dy.ptr, M * 4, stream)
+        H.sync(stream)
+        return np.ascontiguousarray(dy.read())
+
+    announce("qmatvec stream workspaces: 64 streams released, 12 kept")
+    ref = call(None)
+    assert O.row_l2_error(ref, oracle_qmatvec(t, raw, K, M, X)) <= TOL
+    start = mem_free()
+    for _ in range(64):
+        s = Stream()
+        assert np.array_equal(call(s.handle).view(np.uint32), ref.view(np.uint32))
+        s.close()  # trc_hip_qmatvec_release_stream, then hipStreamDestroy
+    assert abs(mem_free() - start) <= 1 << 20
+    live = [Stream() for _ in range(12)]
+    before = mem_free()  # after the streams' own allocations
+    for s in live:
+        assert np.array_equal(call(s.handle).view(np.uint32), ref.view(np.uint32))
+    ws_bound = 12 << 20  # one workspace (8.3 MiB) with the allocator's rounding
+    grown = before - mem_free()
+    print(f"12 live streams: workspaces took {grown / 2**20:.1f} MiB", flush=True)
+    assert grown <= 8 * ws_bound
+    for s in live:
+        s.close()
+    H.qmatvec_release_stream(None)
+    assert mem_free() >= start - (1 << 20)
+    H.qmatvec_release_stream(None)  # nothing left to free: still OK
+    for d in (dw, dx, dy):
+        d.free()
 
 
 def _random_cases(n=48, seed=20261202):

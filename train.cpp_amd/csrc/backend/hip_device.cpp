@@ -268,7 +268,9 @@ public:
     void select() const { check(trc_hip_init(ordinal_, nullptr), "select device"); }
     int ordinal() const { return ordinal_; }
 
-    // Device scratch that grows on demand (released with the device).
+    // Device scratch for graph computation (src0 planes dequantized for wide
+    // right-hand sides): grows on demand and is kept for the next graph, released
+    // with the device. GGUF staging uses buffers of its own (StagingBuffer).
     uint8_t* scratch(size_t bytes) {
         if (bytes > scratch_size_) {
             if (scratch_ != nullptr) {
@@ -483,6 +485,21 @@ Device* hip_device(int ordinal) {
 
 // ---- hooks used by the GGUF reader (core/hip_hooks.h) ----
 
+namespace {
+// Device memory for one GGUF staging call, freed when the call returns (after
+// its synchronous copies), so loading a large tensor does not leave the device
+// scratch that graph computation keeps grown to its size.
+struct StagingBuffer {
+    void* p = nullptr;
+    explicit StagingBuffer(size_t bytes) { check(trc_hip_malloc(&p, bytes), "GGUF staging allocation"); }
+    ~StagingBuffer() {
+        if (p != nullptr) trc_hip_free(p);
+    }
+    StagingBuffer(const StagingBuffer&) = delete;
+    StagingBuffer& operator=(const StagingBuffer&) = delete;
+};
+}  // namespace
+
 bool hip_dequant_into(Tensor* dst, Type type, const void* host_blocks, int64_t n_blocks) {
     HipBuffer* buf = hip_buffer_of(dst);
     if (buf == nullptr || !legacy_quant(type) || dst->type != TYPE_F32 || !tensor_is_contiguous(dst) ||
@@ -492,7 +509,8 @@ bool hip_dequant_into(Tensor* dst, Type type, const void* host_blocks, int64_t n
     HipDevice* dev = static_cast<HipDevice*>(buf->buffer_type()->device());
     dev->select();
     const size_t raw = (size_t) n_blocks * type_size(type);
-    uint8_t* staging = dev->scratch(raw);
+    StagingBuffer buf_raw(raw);
+    uint8_t* staging = (uint8_t*) buf_raw.p;
     check(trc_hip_h2d(staging, host_blocks, raw, nullptr), "gguf_load_tensor (upload blocks)");
     check(trc_hip_dequant((int) type, staging, n_blocks, (float*) buf->address(dst), nullptr),
           "gguf_load_tensor (dequantize)");
@@ -549,7 +567,8 @@ bool hip_dequant_host(Type type, const void* host_blocks, int64_t n_blocks, floa
     dev->select();
     const size_t raw = (size_t) n_blocks * type_size(type);
     const size_t raw_aligned = (raw + 255) / 256 * 256;
-    uint8_t* s = dev->scratch(raw_aligned + (size_t) n_blocks * 32 * sizeof(float));
+    StagingBuffer buf(raw_aligned + (size_t) n_blocks * 32 * sizeof(float));
+    uint8_t* s = (uint8_t*) buf.p;
     check(trc_hip_h2d(s, host_blocks, raw, nullptr), "gguf_tensor_to_f32 (upload blocks)");
     check(trc_hip_dequant((int) type, s, n_blocks, (float*) (s + raw_aligned), nullptr),
           "gguf_tensor_to_f32 (dequantize)");

@@ -293,6 +293,11 @@ int trc_hip_qmatvec_noalloc(int type, const void* wq, int64_t K, int64_t M, size
     return launch_qmatvec(type, wq, K, M, nb1_w, x, N, nb1_x, y, nb1_y, (hipStream_t) stream, QmScratch::STATIC);
 }
 
+int trc_hip_qmatvec_release_stream(void* stream) {
+    TRC_FORCED("trc_hip_qmatvec_release_stream");
+    return qm_release_stream((hipStream_t) stream);
+}
+
 int trc_hip_cpy(const trc_hip_tensor* src, const trc_hip_tensor* dst, void* stream) {
     TRC_FORCED("trc_hip_cpy");
     if (src == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_cpy: NULL tensor");

@@ -66,6 +66,8 @@ size_t qm_workspace_bytes();
 int qm_scratch_setup();
 int qm_static_scratch(uint8_t** ws);
 int qm_stream_workspace(hipStream_t stream, uint8_t** ws);
+// Waits for `stream` and frees its workspace on the current device (if any).
+int qm_release_stream(hipStream_t stream);
 int launch_add_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t stream);
 int launch_mul_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t stream);
 int launch_repeat_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t stream);

@@ -918,13 +918,19 @@ bool qm_lx_fits(const QmPlan& p) {
 // beside the ring, each workgroup converts x itself and no pre-pass runs.
 template <int TYPE, int NT, bool PK>
 int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
-               size_t nb1_y, uint8_t* ws, hipStream_t s) {
+               size_t nb1_y, QmScratch where, hipStream_t s) {
     const QmPlan p = qm_plan<TYPE, NT>(nblk, M);
-    const QmCall q{wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts, p.part_chunks, ws, x, nb1_x, s};
     const int tiles = (p.rows + 15) / 16;
     if constexpr (PK) {
-        if (qm_lx_fits<TYPE>(p)) return launch_tiles<TYPE, 1, NT, PK, QM_LXC>(tiles, q);
+        if (qm_lx_fits<TYPE>(p)) {  // x converted in the kernel: no workspace
+            const QmCall q{wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts, p.part_chunks, nullptr, x, nb1_x, s};
+            return launch_tiles<TYPE, 1, NT, PK, QM_LXC>(tiles, q);
+        }
     }
+    uint8_t* ws = nullptr;
+    const int wrc = where == QmScratch::STATIC ? qm_static_scratch(&ws) : qm_stream_workspace(s, &ws);
+    if (wrc != TRC_HIP_OK) return wrc;
+    const QmCall q{wq, nblk, M, nb1_w, y, nb1_y, N, p.rows, p.parts, p.part_chunks, ws, x, nb1_x, s};
     const int nchunks = (nblk + QM_CHB - 1) / QM_CHB;
     const int ncol = PK ? 8 : 16 * NT;  // one pre-pass wave per chunk and column
     hipLaunchKernelGGL(k_qmm_xprep, dim3((unsigned) (nchunks * ncol)), dim3(64), 0, s, x,
@@ -937,10 +943,10 @@ int launch_fmt(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x
 
 template <int TYPE>
 int launch_cols(const void* wq, int nblk, int64_t M, size_t nb1_w, const float* x, size_t nb1_x, int N, float* y,
-                size_t nb1_y, uint8_t* ws, hipStream_t s) {
-    if (N > 16) return launch_fmt<TYPE, 2, false>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
-    if (N > 8) return launch_fmt<TYPE, 1, false>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
-    return launch_fmt<TYPE, 1, true>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, ws, s);
+                size_t nb1_y, QmScratch where, hipStream_t s) {
+    if (N > 16) return launch_fmt<TYPE, 2, false>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, where, s);
+    if (N > 8) return launch_fmt<TYPE, 1, false>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, where, s);
+    return launch_fmt<TYPE, 1, true>(wq, nblk, M, nb1_w, x, nb1_x, N, y, nb1_y, where, s);
 }
 
 }  // namespace
@@ -961,15 +967,12 @@ int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, con
         return fail(TRC_HIP_E_SHAPE, "qmm: K = %lld exceeds the %d the x workspace holds", (long long) K,
                     QM_MAX_BLOCKS * QK);
     }
-    uint8_t* ws = nullptr;
-    const int rc = where == QmScratch::STATIC ? qm_static_scratch(&ws) : qm_stream_workspace(s, &ws);
-    if (rc != TRC_HIP_OK) return rc;
     switch (type) {
-        case TRC_HIP_TYPE_Q4_0: return launch_cols<TRC_HIP_TYPE_Q4_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
-        case TRC_HIP_TYPE_Q4_1: return launch_cols<TRC_HIP_TYPE_Q4_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
-        case TRC_HIP_TYPE_Q5_0: return launch_cols<TRC_HIP_TYPE_Q5_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
-        case TRC_HIP_TYPE_Q5_1: return launch_cols<TRC_HIP_TYPE_Q5_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
-        case TRC_HIP_TYPE_Q8_0: return launch_cols<TRC_HIP_TYPE_Q8_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, ws, s);
+        case TRC_HIP_TYPE_Q4_0: return launch_cols<TRC_HIP_TYPE_Q4_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, where, s);
+        case TRC_HIP_TYPE_Q4_1: return launch_cols<TRC_HIP_TYPE_Q4_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, where, s);
+        case TRC_HIP_TYPE_Q5_0: return launch_cols<TRC_HIP_TYPE_Q5_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, where, s);
+        case TRC_HIP_TYPE_Q5_1: return launch_cols<TRC_HIP_TYPE_Q5_1>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, where, s);
+        case TRC_HIP_TYPE_Q8_0: return launch_cols<TRC_HIP_TYPE_Q8_0>(wq, nblk, M, nb1_w, x, nb1_x, (int) N, y, nb1_y, where, s);
         default: return fail(TRC_HIP_E_INVALID, "qmm: bad type %d", type);
     }
 }
@@ -979,10 +982,13 @@ int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, con
 // ---------------------------------------------------------------- x workspaces
 //
 // trc_hip_qmatvec: one workspace per (device, stream), allocated by the first
-// call on that stream that takes this path and kept until the process ends.
-// Work on one stream runs in order, so calls on different streams never share
-// x planes. hipStreamPerThread names a different stream in every host thread,
-// so its workspaces are also keyed by thread.
+// call on that stream whose shape runs the x pre-pass, and kept for later calls
+// on the stream. Work on one stream runs in order, so calls on different
+// streams never share x planes. hipStreamPerThread names a different stream in
+// every host thread, so its workspaces are also keyed by thread. At most
+// QM_STREAM_WS workspaces are kept per device: a new stream past that waits for
+// the device to go idle and takes over the least recently used one.
+// trc_hip_qmatvec_release_stream frees a stream's workspace after its work.
 //
 // trc_hip_qmatvec_noalloc: the file-scope device array `scratch` below. Each GPU
 // holds its own copy at its own address, found once per device with
@@ -1005,6 +1011,7 @@ namespace trc_hip {
 namespace {
 
 constexpr int QM_MAX_DEV = 64;
+constexpr int QM_STREAM_WS = 8;  // per-stream workspaces kept per device
 std::mutex g_ws_mutex;
 uint8_t* g_scratch_dev[QM_MAX_DEV] = {};  // address of `scratch` on each device, once resolved
 
@@ -1013,17 +1020,23 @@ struct StreamWs {
     hipStream_t stream;
     std::thread::id thread;  // only for hipStreamPerThread
     uint8_t* ptr;
+    uint64_t last_use;
 };
 std::vector<StreamWs>& stream_workspaces() {
     static std::vector<StreamWs> v;
     return v;
 }
+uint64_t g_ws_clock = 0;
 
 int current_device(int* dev) {
     const hipError_t e = hipGetDevice(dev);
     if (e != hipSuccess) return hip_error(e, "hipGetDevice");
     if (*dev < 0 || *dev >= QM_MAX_DEV) return fail(TRC_HIP_E_NO_DEVICE, "device %d out of range", *dev);
     return TRC_HIP_OK;
+}
+
+std::thread::id stream_thread(hipStream_t s) {
+    return s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
 }
 
 }  // namespace
@@ -1061,19 +1074,56 @@ int qm_stream_workspace(hipStream_t s, uint8_t** ws) {
     int dev = 0;
     const int rc = current_device(&dev);
     if (rc != TRC_HIP_OK) return rc;
-    const std::thread::id tid = s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+    const std::thread::id tid = stream_thread(s);
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    for (const StreamWs& w : stream_workspaces()) {
-        if (w.dev == dev && w.stream == s && w.thread == tid) {
+    std::vector<StreamWs>& v = stream_workspaces();
+    int on_dev = 0;
+    StreamWs* lru = nullptr;
+    for (StreamWs& w : v) {
+        if (w.dev != dev) continue;
+        if (w.stream == s && w.thread == tid) {
+            w.last_use = ++g_ws_clock;
             *ws = w.ptr;
             return TRC_HIP_OK;
         }
+        ++on_dev;
+        if (lru == nullptr || w.last_use < lru->last_use) lru = &w;
+    }
+    if (on_dev >= QM_STREAM_WS) {
+        // the least recently used stream's last call may still be running: wait
+        // for the device, then hand its workspace to this stream
+        const hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_error(e, "qmatvec: waiting for the device to reuse an x workspace");
+        lru->stream = s;
+        lru->thread = tid;
+        lru->last_use = ++g_ws_clock;
+        *ws = lru->ptr;
+        return TRC_HIP_OK;
     }
     void* p = nullptr;
     const hipError_t e = hipMalloc(&p, QM_WS_BYTES);
     if (e != hipSuccess) return hip_error(e, "qmatvec: x workspace for a new stream (hipMalloc)");
-    stream_workspaces().push_back({dev, s, tid, (uint8_t*) p});
+    v.push_back({dev, s, tid, (uint8_t*) p, ++g_ws_clock});
     *ws = (uint8_t*) p;
+    return TRC_HIP_OK;
+}
+
+int qm_release_stream(hipStream_t s) {
+    int dev = 0;
+    int rc = current_device(&dev);
+    if (rc != TRC_HIP_OK) return rc;
+    const std::thread::id tid = stream_thread(s);
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    std::vector<StreamWs>& v = stream_workspaces();
+    for (size_t i = 0; i < v.size(); ++i) {
+        if (v[i].dev != dev || v[i].stream != s || v[i].thread != tid) continue;
+        // the stream's last calls may still read the workspace
+        rc = hip_error(hipStreamSynchronize(s), "qmatvec_release_stream: hipStreamSynchronize");
+        if (rc != TRC_HIP_OK) return rc;
+        rc = hip_error(hipFree(v[i].ptr), "qmatvec_release_stream: hipFree");
+        v.erase(v.begin() + (long) i);
+        return rc;
+    }
     return TRC_HIP_OK;
 }
 

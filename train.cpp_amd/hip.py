@@ -24,7 +24,7 @@ EXPORTS = (
     "trc_hip_malloc", "trc_hip_free", "trc_hip_h2d", "trc_hip_d2h", "trc_hip_memset",
     "trc_hip_fill_f32", "trc_hip_dequant", "trc_hip_mul_mat_f32", "trc_hip_qmatvec", "trc_hip_cpy",
     "trc_hip_add_f32", "trc_hip_acc_f32", "trc_hip_repeat_back_f32", "trc_hip_qmatvec_noalloc",
-    "trc_hip_mul_f32", "trc_hip_repeat_f32", "trc_hip_sum_f32",
+    "trc_hip_mul_f32", "trc_hip_repeat_f32", "trc_hip_sum_f32", "trc_hip_qmatvec_release_stream",
 )
 
 
@@ -94,6 +94,7 @@ def load() -> C.CDLL:
         "trc_hip_mul_mat_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_qmatvec": ([I, P, I64, I64, SZ, P, I64, SZ, P, SZ, P], I),
         "trc_hip_qmatvec_noalloc": ([I, P, I64, I64, SZ, P, I64, SZ, P, SZ, P], I),
+        "trc_hip_qmatvec_release_stream": ([P], I),
         "trc_hip_cpy": ([C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_add_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_acc_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), SZ, SZ, SZ, SZ, I, P], I),
@@ -148,6 +149,10 @@ def mul_mat_f32(a: Tensor, b: Tensor, d: Tensor, stream: int | None = None) -> N
 def qmatvec(type_: int, w_ptr: int, K: int, M: int, nb1_w: int, x_ptr: int, N: int, nb1_x: int,
             y_ptr: int, nb1_y: int, stream: int | None = None) -> None:
     check(load().trc_hip_qmatvec(type_, w_ptr, K, M, nb1_w, x_ptr, N, nb1_x, y_ptr, nb1_y, stream))
+
+
+def qmatvec_release_stream(stream: int | None = None) -> None:
+    check(load().trc_hip_qmatvec_release_stream(stream))
 
 
 def qmatvec_noalloc(type_: int, w_ptr: int, K: int, M: int, nb1_w: int, x_ptr: int, N: int, nb1_x: int,
