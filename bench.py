@@ -283,6 +283,88 @@ def mul_mat_config4(H, synth, timer, steps, warmup):
             "timing": mode}
 
 
+def linear_step(H, synth, timer, steps, warmup):
+    """One training step of configuration 3's Linear layer with bias and the loss
+    L = sum(mul(y, g)): the kernels HipDevice::graph_compute runs for the graph
+    the reference's autograd builds (src/core/trc_autograd.cpp: graph_reset's
+    fills, then mul_mat, add, mul, sum, repeat, mul, repeat_back, acc, the
+    transposed mul_mat of dW^T, cont, acc, the transposed mul_mat of dX, acc), in
+    that order through the C ABI on one stream. Reported per step, with the
+    products' share."""
+    K = M = 4096
+    T = 512
+    f4 = 4
+    n = K * M // 32
+    q = synth.block_bytes(synth.quant_blocks(7, n, synth.config_seed(3, 0)))
+    qd = H.DeviceBuffer(q.nbytes).upload(q)
+    bufs = {}
+
+    def buf(name, nfloat):
+        bufs[name] = H.DeviceBuffer(max(nfloat, 4) * 4)
+        return bufs[name]
+
+    Wd = buf("W", K * M)
+    H.dequant(7, qd.ptr, n, Wd.ptr)
+    H.sync()
+    qd.free()
+    Xd = buf("X", K * T).upload(synth.normal(synth.config_seed(3, 1), K * T))
+    bd = buf("b", M).upload(synth.normal(synth.config_seed(3, 3), M))
+    Gd = buf("G", M * T).upload(synth.normal(synth.config_seed(3, 2), M * T, 0.0, 1e-2))
+    for name, nf in (("MM", M * T), ("Y", M * T), ("YG", M * T), ("L", 1), ("dL", 1), ("R", M * T), ("DY", M * T),
+                     ("DB", M), ("DWt", M * K), ("DWc", K * M), ("DX", K * T), ("gW", K * M), ("gX", K * T),
+                     ("gb", M)):
+        buf(name, nf)
+
+    def t(name, ne, nb=None):
+        return H.tensor(bufs[name].ptr, ne, nb if nb is not None else H.contiguous_nb(ne))
+
+    W, X, b, G = t("W", [K, M, 1, 1]), t("X", [K, T, 1, 1]), t("b", [M, 1, 1, 1]), t("G", [M, T, 1, 1])
+    MM, Y, YG = t("MM", [M, T, 1, 1]), t("Y", [M, T, 1, 1]), t("YG", [M, T, 1, 1])
+    L, dL, R, DY = t("L", [1, 1, 1, 1]), t("dL", [1, 1, 1, 1]), t("R", [M, T, 1, 1]), t("DY", [M, T, 1, 1])
+    DB, gb = t("DB", [M, 1, 1, 1]), t("gb", [M, 1, 1, 1])
+    DYt = t("DY", [T, M, 1, 1], [M * f4, f4, M * T * f4, M * T * f4])
+    Xt = t("X", [T, K, 1, 1], [K * f4, f4, K * T * f4, K * T * f4])
+    DWt = t("DWt", [M, K, 1, 1])
+    DWt_t = t("DWt", [K, M, 1, 1], [M * f4, f4, M * K * f4, M * K * f4])
+    DWc, gW = t("DWc", [K, M, 1, 1]), t("gW", [K, M, 1, 1])
+    Wt = t("W", [M, K, 1, 1], [K * f4, f4, K * M * f4, K * M * f4])
+    DX, gX = t("DX", [K, T, 1, 1]), t("gX", [K, T, 1, 1])
+
+    def step(i, s):
+        # graph_reset: gradient accumulators to 0, the loss gradient to 1
+        H.fill_f32(bufs["gW"].ptr, 0.0, K * M, s)
+        H.fill_f32(bufs["gX"].ptr, 0.0, K * T, s)
+        H.fill_f32(bufs["gb"].ptr, 0.0, M, s)
+        H.fill_f32(bufs["dL"].ptr, 1.0, 1, s)
+        # forward
+        H.mul_mat_f32(W, X, MM, s)
+        H.add_f32(MM, b, Y, s)
+        H.mul_f32(Y, G, YG, s)
+        H.sum_f32(YG, L, s)
+        # backward
+        H.repeat_f32(dL, R, s)
+        H.mul_f32(R, G, DY, s)
+        H.repeat_back_f32(DY, DB, s)
+        H.acc_f32(gb, DB, gb, M * f4, M * f4, M * f4, 0, True, s)
+        H.mul_mat_f32(DYt, Xt, DWt, s)
+        H.cpy(DWt_t, DWc, s)
+        H.acc_f32(gW, DWc, gW, K * f4, K * M * f4, K * M * f4, 0, True, s)
+        H.mul_mat_f32(Wt, DY, DX, s)
+        H.acc_f32(gX, DX, gX, K * f4, K * T * f4, K * T * f4, 0, True, s)
+
+    ms, mode = timer.run(step, steps, warmup)
+    prods = {}
+    for name, (a, bb, d) in {"fwd": (W, X, MM), "dW^T": (DYt, Xt, DWt), "dX": (Wt, DY, DX)}.items():
+        pm, _ = timer.run(lambda i, s, a=a, bb=bb, d=d: H.mul_mat_f32(a, bb, d, s), steps, warmup)
+        prods[name] = round(pm * 1e3, 2)
+    for v in bufs.values():
+        v.free()
+    fl = 3 * 2.0 * K * M * T
+    return {"us": ms * 1e3, "products_us": prods, "products_sum_us": round(sum(prods.values()), 2),
+            "other_kernels_us": round(ms * 1e3 - sum(prods.values()), 2), "TFLOP/s": fl / (ms * 1e-3) / 1e12,
+            "frac_mfma": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFS, "timing": mode, "kernel_launches": 17}
+
+
 def mul_mat_config0(H, synth, timer, N, steps, warmup):
     """Configuration 0's product after the GGUF warm start: W F32 [4096, 4096] (the
     GPU dequant of the Q8_0 blocks) times X F32 [4096, N] through
@@ -572,11 +654,12 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time a 256 MiB device copy (reference for the traffic counters)")
-    ap.add_argument("--only", choices=["dequant", "mul_mat", "qmm", "cfg0", "qmm_sweep", "mm0", "mm0_sweep"],
+    ap.add_argument("--only", choices=["dequant", "mul_mat", "qmm", "cfg0", "qmm_sweep", "mm0", "mm0_sweep", "step"],
                     help="only time one hot path and print its figures (for counter runs): dequant = the five "
                          "formats on configuration 1, mul_mat = configurations 3 and 4, qmm = Q4_0 N=16 on "
                          "configuration 2, qmm_sweep = Q4_0 on configuration 2 for N from 1 to 64, mm0 = "
-                         "configuration 0's F32 product (8 columns), mm0_sweep = the same for N from 1 to 64")
+                         "configuration 0's F32 product (8 columns), mm0_sweep = the same for N from 1 to 64, step = "
+                         "configuration 3's Linear training step")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; multi-GPU runs are not part of this "
@@ -603,6 +686,8 @@ def main():
             part["cfg4"] = mul_mat_config4(H, synth, timer, args.steps, args.warmup)
         elif args.only == "qmm":
             part["q4_0 N=16"], _, _ = qmatvec_case(H, synth, timer, H.TYPE_Q4_0, K, M, 16, args.steps, args.warmup)
+        elif args.only == "step":
+            part["linear_step"] = linear_step(H, synth, timer, args.steps, args.warmup)
         elif args.only == "mm0":
             part["N=8"] = mul_mat_config0(H, synth, timer, 8, args.steps, args.warmup)
         elif args.only == "mm0_sweep":
@@ -659,6 +744,7 @@ def main():
             extra["dequant_4096x11008"][name] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
         extra["mul_mat_cfg3_linear_4096x4096x512"] = mul_mat_config3(H, synth, timer, max(10, s // 4), 3)
         extra["mul_mat_cfg4_batched_permuted"] = mul_mat_config4(H, synth, timer, max(10, s // 4), 3)
+        extra["linear_step_cfg3_fwd_bwd"] = linear_step(H, synth, timer, max(10, s // 4), 3)
         extra["gguf_load_cfg0_hip_route"] = gguf_load_cfg0(H, synth)
 
     host = cpu_host_info()

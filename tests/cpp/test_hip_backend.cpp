@@ -846,8 +846,14 @@ void test_gguf_reader_cpu(const std::string& dir) {
             EXPECT(p64 != nullptr && n == 3 && p64[0] == 1 && p64[1] == -5 && p64[2] == 1099511627776ll);
             EXPECT(std::string(gguf_get_arr_str(f, "t.arr_str", 1)) == "\xe8\xb4\x9d\xe5\xa1\x94");
             EXPECT(gguf_get_arr_str(f, "t.arr_str", 2) == nullptr);       // index out of range
-            EXPECT(gguf_get_arr_i32(f, "t.arr_f32", &n) == nullptr);     // wrong element type
+            n = 77;
+            EXPECT(gguf_get_arr_i32(f, "t.arr_f32", &n) == nullptr && n == 77);  // wrong element type, n untouched
+            EXPECT(gguf_get_arr_f32(f, "t.u32", &n) == nullptr && n == 77);      // not an array, n untouched
             EXPECT(gguf_get_u32(f, "t.i32") == 0);                       // wrong scalar type
+            // probing a scalar key for array-ness logs an error and answers U8 / 0
+            // (src/io/trc_gguf.cpp:814-834) instead of aborting
+            const int64_t sidx = gguf_find_key(f, "t.u32");
+            EXPECT(sidx >= 0 && gguf_arr_type(f, sidx) == GgufType::U8 && gguf_arr_count(f, sidx) == 0);
             const int64_t idx = gguf_find_key(f, "t.arr_str");
             EXPECT(idx >= 0 && gguf_kv_type(f, idx) == GgufType::ARRAY && gguf_arr_type(f, idx) == GgufType::STRING &&
                    gguf_arr_count(f, idx) == 2 && std::string(gguf_key(f, idx)) == "t.arr_str");

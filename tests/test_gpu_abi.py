@@ -64,6 +64,22 @@ def test_cpy_transpose_is_cont(hip, dtype):
     assert np.array_equal(out.read(), np.ascontiguousarray(np.swapaxes(x, 2, 3)))
 
 
+@pytest.mark.parametrize("shape", [(2, 3, 70, 130), (1, 1, 4096, 4096), (1, 1, 1, 65), (1, 1, 65, 1)])
+def test_cpy_transpose_tiles(hip, shape):
+    """4-byte transposes through the LDS tiles: ragged tiles over planes, the
+    Linear layer's 64 MiB dW^T, and single rows or columns (plain copy path)."""
+    announce(f"abi cpy transpose {shape}")
+    x = np.random.default_rng(3).standard_normal(shape).astype(np.float32)
+    src = Dev(x)
+    view = np.swapaxes(src.base, 2, 3)
+    out = empty(view.shape, np.float32)
+    H.cpy(src.tensor(view), out.tensor())
+    H.sync()
+    assert np.array_equal(out.read().view(np.uint32), np.ascontiguousarray(np.swapaxes(x, 2, 3)).view(np.uint32))
+    src.free()
+    out.free()
+
+
 def test_forced_error_hook(hip):
     os.environ["TRC_HIP_FORCE_ERROR"] = "trc_hip_dequant"
     try:

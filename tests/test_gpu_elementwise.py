@@ -44,6 +44,22 @@ def test_add_broadcast_bitwise(hip, bshape):
     assert (bits(got) == bits(O.add(a, b))).all()
 
 
+@pytest.mark.parametrize("bshape", [(3, 5, 7, 64), (1, 5, 7, 64), (3, 1, 7, 1), (1, 1, 1, 64), (3, 5, 1, 1),
+                                    (1, 1, 1, 1)])
+@pytest.mark.parametrize("op", ["add", "mul"])
+def test_binary_four_floats_per_lane_bitwise(hip, bshape, op):
+    """Rows of 64 floats, 16-byte aligned: the kernel that reads and writes four
+    floats per lane, with b broadcast along every dim (scalar per row along ne0)."""
+    announce(f"{op} vec4 bcast {bshape}")
+    rng = np.random.default_rng(14)
+    a = rng.standard_normal((3, 5, 7, 64)).astype(np.float32)
+    b = rng.standard_normal(bshape).astype(np.float32)
+    if op == "add":
+        assert (bits(gpu_add(a, a, b, b)) == bits(O.add(a, b))).all()
+    else:
+        assert (bits(gpu_mul(a, a, b, b)) == bits(O.mul(a, b))).all()
+
+
 def test_add_strided_views_bitwise(hip):
     rng = np.random.default_rng(12)
     A = rng.standard_normal((4, 6, 300, 9)).astype(np.float32)
@@ -139,6 +155,33 @@ def test_repeat_back_bitwise(hip, d_ne):
         assert (bits(got) == bits(O.repeat_back(view, d_ne))).all()
 
 
+@pytest.mark.parametrize("a_shape,d_ne", [((512, 4096), [4096, 1, 1, 1]), ((6, 4, 6, 8), [8, 3, 2, 3]),
+                                          ((1000, 64), [64, 1, 1, 1]), ((130, 100), [100, 1, 1, 1]),
+                                          ((300, 70), [70, 3, 1, 1]),
+                                          ((5, 3, 70, 33), [33, 7, 1, 1]), ((2, 1000, 64), [64, 1, 1, 1])])
+def test_repeat_back_columns_bitwise(hip, a_shape, d_ne):
+    """ne0 not repeated (the Linear layer's db: [4096, 512] back to [4096, 1]), with
+    repeats along one, two or three dims, plain and transposed-plane views."""
+    announce(f"repeat_back columns {a_shape} -> {d_ne}")
+    rng = np.random.default_rng(17)
+    A = rng.standard_normal(a_shape).astype(np.float32)
+    views = [A]
+    if A.ndim == 4 and A.shape[0] == A.shape[2]:
+        views.append(A.transpose(2, 1, 0, 3))  # swap ggml dims 1 and 3 (nb3 < nb1)
+    for view in views:
+        ne, _ = O.view_meta(view)
+        if any(ne[k] % d_ne[k] for k in range(4)):
+            continue
+        da = Dev(A)
+        out = empty(O.ggml_shape(d_ne))
+        H.repeat_back_f32(da.tensor(view), out.tensor())
+        H.sync()
+        got = out.read()
+        da.free()
+        out.free()
+        assert (bits(got) == bits(O.repeat_back(view, d_ne))).all()
+
+
 def test_repeat_back_mul_mat_broadcast_shape(hip):
     """The shape mul_mat's backward reduces: dA of configuration 4
     ([128, 1024, 32, 4] summed back to src0's [128, 1024, 8, 4])."""
@@ -203,6 +246,7 @@ def gpu_repeat(a_base, a_view, d_ne):
 
 
 @pytest.mark.parametrize("ashape,d_ne", [((1, 1, 1, 1), [4096, 512, 1, 1]), ((1, 1, 1, 7), [7, 33, 5, 3]),
+                                         ((1, 1, 3, 8), [16, 6, 2, 1]), ((1, 2, 1, 1), [12, 5, 4, 1]),
                                          ((3, 1, 5, 1), [9, 5, 1, 3]), ((1, 1, 1, 1), [1, 1, 1, 1])])
 def test_repeat_bitwise(hip, ashape, d_ne):
     announce(f"repeat {ashape} -> {d_ne}")
@@ -237,6 +281,21 @@ def test_sum_bitwise(hip, shape):
     rng = np.random.default_rng(25)
     a = (rng.standard_normal(shape) * 10.0 ** rng.integers(-3, 4, shape)).astype(np.float32)
     assert bits(gpu_sum(a, a)) == bits(O.sum_all(a))
+
+
+@pytest.mark.parametrize("shape,cut", [((300, 36), None), ((100, 4), None), ((65, 8200), None), ((100, 4), 2),
+                                       ((9, 1000), None), ((3, 2, 17, 256), None), ((5000, 8), None),
+                                       ((4100, 260), None),
+                                       ((70, 4096), 4093), ((1_200_000, 1), None)])
+def test_sum_row_paths_bitwise(hip, shape, cut):
+    """Rows read four floats at a time (16-byte aligned rows) with row lengths that
+    leave partial batches and tails, rows cut shorter than their stride, and more
+    rows than the row-sum workspace holds (the one-workgroup kernel)."""
+    announce(f"sum rows {shape} cut {cut}")
+    rng = np.random.default_rng(27)
+    a = (rng.standard_normal(shape) * 10.0 ** rng.integers(-3, 4, shape)).astype(np.float32)
+    av = a if cut is None else a[..., :cut]
+    assert bits(gpu_sum(a, av)) == bits(O.sum_all(av))
 
 
 def test_sum_order_and_strides_bitwise(hip):

@@ -273,17 +273,25 @@ GgufType gguf_kv_type(const GgufFile* f, int64_t index) {
 
 bool gguf_has_key(const GgufFile* f, const char* key) { return gguf_find_key(f, key) >= 0; }
 
+// A key that is not an array is an error the caller may probe for: it is
+// logged and answered with U8 / 0, as in src/io/trc_gguf.cpp:814-834.
 GgufType gguf_arr_type(const GgufFile* f, int64_t index) {
     TRC_CHECK(index >= 0 && index < (int64_t) f->kvs.size(), "gguf_arr_type: index out of range");
     const GgufKvEntry& kv = f->kvs[(size_t) index];
-    TRC_CHECK(kv.type == GgufType::ARRAY, "gguf_arr_type: key %s is not an array", kv.key.c_str());
+    if (kv.type != GgufType::ARRAY) {
+        log_error("GGUF: key %s is not an array", kv.key.c_str());
+        return GgufType::U8;
+    }
     return kv.arr_type;
 }
 
 int64_t gguf_arr_count(const GgufFile* f, int64_t index) {
     TRC_CHECK(index >= 0 && index < (int64_t) f->kvs.size(), "gguf_arr_count: index out of range");
     const GgufKvEntry& kv = f->kvs[(size_t) index];
-    TRC_CHECK(kv.type == GgufType::ARRAY, "gguf_arr_count: key %s is not an array", kv.key.c_str());
+    if (kv.type != GgufType::ARRAY) {
+        log_error("GGUF: key %s is not an array", kv.key.c_str());
+        return 0;
+    }
     return (int64_t) kv.arr_n;
 }
 
@@ -353,8 +361,9 @@ const GgufKvEntry* typed_arr(const GgufFile* f, const char* key, GgufType elem) 
 template <typename T>
 const T* scalar_array(const GgufFile* f, const char* key, GgufType elem, int64_t* n) {
     const GgufKvEntry* kv = typed_arr(f, key, elem);
-    if (n != nullptr) *n = kv ? (int64_t) kv->arr_n : 0;
-    return kv ? (const T*) kv->arr_words.data() : nullptr;
+    if (kv == nullptr) return nullptr;  // *n untouched, as in src/io/trc_gguf.cpp:900-931
+    if (n != nullptr) *n = (int64_t) kv->arr_n;
+    return (const T*) kv->arr_words.data();
 }
 
 }  // namespace
