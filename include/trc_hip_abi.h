@@ -179,8 +179,9 @@ int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w
 /* Frees the x workspace trc_hip_qmatvec keeps for `stream` on the current
  * device, after waiting for the stream's queued work (hipStreamSynchronize).
  * Call it before hipStreamDestroy; a later call on the stream allocates a new
- * workspace. hipStreamPerThread is keyed by the calling thread. Returns
- * TRC_HIP_OK when the stream has no workspace. No counterpart in the reference:
+ * workspace. trc_hip_sum_f32 keeps its row sums in the same workspace.
+ * hipStreamPerThread is keyed by the calling thread. Returns TRC_HIP_OK when
+ * the stream has no workspace. No counterpart in the reference:
  * it bounds the memory of trc_hip_qmatvec's per-stream workspaces, like the
  * ownership rule of Buffer (include/traincpp/trc_backend.h:33-88). */
 int trc_hip_qmatvec_release_stream(void* stream);
@@ -229,8 +230,11 @@ int trc_hip_repeat_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void*
  * (src/backends/cpu/trc_cpu_ops.cpp:302-315, row_sum_f32 :284-300): each row
  * (ne0-run) is summed in double from 0 in element order, the row sums are added
  * in double in row order, and the total is rounded to float once; the same
- * operations in the same order, so the result is bit-identical. One workgroup:
- * meant for losses, not bulk reductions. */
+ * operations in the same order, so the result is bit-identical. Rows are summed
+ * in parallel (each row's own sum stays sequential) into the stream's x
+ * workspace of trc_hip_qmatvec, which the first such call on a stream allocates
+ * (make it before capturing that stream in global mode); more rows than that
+ * workspace holds (about a million) are summed by one workgroup. */
 int trc_hip_sum_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream);
 
 /* ggml acc: dst = a, then dst[offset + i0*4 + i1*nb1 + i2*nb2 + i3*nb3] += b[i]
