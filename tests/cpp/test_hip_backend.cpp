@@ -590,6 +590,25 @@ void test_quantized_misaligned_x(Device* dev, const std::string& dir) {
 
 void test_fill_and_unsupported(Device* dev) {
     std::printf("fill_tensors / supports_op\n");
+    {
+        // a new buffer reads as zeros (the reference's CPU and Vulkan buffers do),
+        // also where an earlier buffer of the same size left other values
+        for (int round = 0; round < 2; ++round) {
+            Context* c0 = context_new(1 << 16);
+            Tensor* z = new_tensor_2d(c0, TYPE_F32, 4096, 64);
+            Buffer* bz = buffer_alloc_ctx_tensors(c0, dev->default_buffer_type());
+            std::vector<float> vz((size_t) tensor_nelements(z), -1.f);
+            tensor_get(z, vz.data(), 0, vz.size() * 4);
+            size_t nonzero = 0;
+            for (float v : vz) nonzero += v != 0.f;
+            EXPECT(nonzero == 0);
+            std::printf("    [%s] new buffer (round %d) reads as zeros\n", nonzero == 0 ? " OK " : "FAIL", round);
+            const std::vector<float> ones(vz.size(), 7.f);
+            tensor_set(z, ones.data(), 0, ones.size() * 4);  // leave values behind for the next round
+            buffer_free(bz);
+            context_free(c0);
+        }
+    }
     Context* ctx = context_new(1 << 16);
     Tensor* a = new_tensor_2d(ctx, TYPE_F32, 1000, 3);
     Tensor* b = new_tensor_1d(ctx, TYPE_F32, 17);

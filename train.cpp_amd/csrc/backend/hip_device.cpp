@@ -451,12 +451,22 @@ Device* HipBufferType::device() const {
     return dev_;
 }
 
+// A new buffer reads as zeros, as the reference's backends guarantee (CpuBuffer
+// memsets its allocation, src/backends/cpu/trc_cpu.cpp:26-33; the Vulkan backend
+// clears device-local memory, src/backends/vulkan/trc_vulkan.cpp:1079-1084):
+// graphs may read a leaf no one has set, such as the result of dup(), which only
+// copies metadata (src/ops/trc_ops.cpp:11-14). Out of memory returns nullptr.
 Buffer* HipBufferType::alloc_buffer(size_t size) {
     HipDevice* d = dev_;
     d->select();
+    const size_t bytes = size == 0 ? 256 : size;
     void* p = nullptr;
-    if (trc_hip_malloc(&p, size == 0 ? 256 : size) != TRC_HIP_OK) return nullptr;
-    return new HipBuffer(this, d->ordinal(), (uint8_t*) p, size == 0 ? 256 : size);
+    if (trc_hip_malloc(&p, bytes) != TRC_HIP_OK) return nullptr;
+    if (trc_hip_memset(p, 0, bytes, nullptr) != TRC_HIP_OK || trc_hip_sync(nullptr) != TRC_HIP_OK) {
+        trc_hip_free(p);
+        return nullptr;
+    }
+    return new HipBuffer(this, d->ordinal(), (uint8_t*) p, bytes);
 }
 
 std::mutex g_devices_mutex;
