@@ -263,7 +263,7 @@ def cfg0_w():
     return O.dequant(H.TYPE_Q8_0, raw, threads=8).reshape(1, 1, 4096, 4096)
 
 
-@pytest.mark.parametrize("N", [1, 2, 3, 8, 16, 32, 64])
+@pytest.mark.parametrize("N", [1, 2, 3, 5, 7, 8, 16, 32, 64])
 @pytest.mark.parametrize("layout", ["contiguous", "transposed"])
 def test_config0_f32_few_columns(hip, cfg0_w, N, layout):
     """mul_mat(W F32 [4096, 4096], X [4096, N]) at configuration 0's size, every dst
@@ -277,6 +277,25 @@ def test_config0_f32_few_columns(hip, cfg0_w, N, layout):
         got, want = run_views(cfg0_w, lambda x: x, X.reshape(1, 1, 4096, N), t01)
     assert got.shape == (1, 1, N, 4096)
     assert O.row_l2_error(got, want) <= TOL
+
+
+@pytest.mark.parametrize("K,M,N", [(512, 16, 1), (4096, 48, 5), (4096, 4096, 8), (1028, 70, 12), (2048, 33, 40)])
+def test_few_columns_one_hot(hip, K, M, N):
+    """W rows with a single 1 at k = kmap[i] and X[j, k] = 1000 j + k: every output
+    is one X element times 1 plus exact zeros, so it must equal 1000 j + kmap[i]
+    bit for bit. A wrong lane-to-(column, k) mapping in the few-column loads shows
+    up here as the value of the (column, k) that was read instead."""
+    announce(f"mul_mat one-hot K={K} M={M} N={N}")
+    kmap = (np.arange(M) * 131 + 7) % K
+    W = np.zeros((1, 1, M, K), np.float32)
+    W[0, 0, np.arange(M), kmap] = 1.0
+    X = (1000.0 * np.arange(N)[:, None] + np.arange(K)[None, :]).astype(np.float32).reshape(1, 1, N, K)
+    a, b = Dev(W), Dev(X)
+    got = gpu_mul_mat(a, W, b, X)
+    want = (1000.0 * np.arange(N)[:, None] + kmap[None, :]).astype(np.float32).reshape(1, 1, N, M)
+    assert np.array_equal(got, want)
+    a.free()
+    b.free()
 
 
 def test_config0_f32_deterministic(hip, cfg0_w):
@@ -294,6 +313,7 @@ def test_config0_f32_deterministic(hip, cfg0_w):
     (4, 1, 1, 1, 1, 1, 1), (36, 17, 5, 1, 1, 1, 1), (100, 33, 16, 1, 1, 1, 1), (512, 70, 17, 1, 1, 1, 1),
     (1028, 250, 33, 1, 1, 1, 1), (2048, 300, 48, 1, 1, 1, 1), (260, 129, 64, 1, 1, 1, 1),
     (128, 64, 8, 4, 2, 2, 1), (96, 48, 24, 6, 1, 3, 1), (64, 40, 64, 2, 2, 1, 2),
+    (1000, 77, 7, 1, 1, 1, 1), (4100, 33, 6, 2, 1, 1, 1),
 ])
 @pytest.mark.parametrize("layout", ["kk", "kt", "kgen", "kmis"])
 def test_few_columns_shapes(hip, shape, layout):

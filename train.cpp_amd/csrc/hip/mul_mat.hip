@@ -278,6 +278,12 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
 //   - Lane l reads row l % 16 of the block at k = 32c + 4g .. +3 and
 //     32c + 16 + 4g .. +3 (g = l / 16): two float4 loads, 64 contiguous bytes
 //     per row and instruction. It reads X column 16t + l % 16 at the same k.
+//   - With 5 to 8 k-contiguous columns, those X loads would fetch half lines for
+//     16 column slots, half of them empty. One load of 8 columns x 32 k (full
+//     128-byte lines; lane 8j + q holds column j at k = 32c + 4q) replaces
+//     the two, and ds_bpermute moves each float to the lane the MFMA wants it
+//     in. The texture path's load count per chunk drops from 4 to 3; cfg0's
+//     N = 8 product went from 16.2 to 15.2 us.
 //   - v_mfma_f32_16x16x4_f32 with X as the A operand (MFMA row = column j of X)
 //     and W as the B operand (MFMA column = row i of W); A and B take the same
 //     k from the same lane, so any k order within a chunk gives the same dot.
@@ -308,6 +314,8 @@ constexpr int SK_WAVES = 16;
 constexpr int SK_MAX_N = 64;
 constexpr uint32_t SK_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
 constexpr uint32_t SK_OUT = 0x80000000u;         // an offset past every resource: the load returns 0
+constexpr int SK_X8 = 3;                          // X mode: k-contiguous, at most 8 columns
+typedef int i4 __attribute__((ext_vector_type(4)));
 
 // One chunk's operands in registers: W (two float4) and X (two float4 per
 // 16-column group).
@@ -332,6 +340,17 @@ __device__ __forceinline__ void sk_load(SkChunk<NT>& c, __amdgpu_buffer_rsrc_t r
     // rows past M lie past rw's range by construction
     c.w0 = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok0 ? wrow_off + 4u * k0 : SK_OUT, 0, 0));
     c.w1 = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok1 ? wrow_off + 4u * k1 : SK_OUT, 0, 0));
+    if constexpr (BMODE == SK_X8) {
+        // up to 8 columns: one load of 8 columns x 32 k, full 128-byte lines; lane
+        // 8c + q holds column c at k = 32 chunk + 4q .. +3 (sk_mfma moves it into place)
+        const int xl = 16 * g + r;
+        const int xc = xl >> 3;
+        const int kx = chunk * 32 + 4 * (xl & 7);
+        const bool cx = chunk_ok && xc < p.N && kx < p.K;
+        const uint32_t off = (uint32_t) xc * (uint32_t) p.b_nb1 + 4u * (uint32_t) kx;
+        c.x0[0] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, cx ? off : SK_OUT, 0, 0));
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int j = 16 * t + r;
@@ -353,8 +372,28 @@ __device__ __forceinline__ void sk_load(SkChunk<NT>& c, __amdgpu_buffer_rsrc_t r
     }
 }
 
-template <int NT>
-__device__ __forceinline__ void sk_mfma(const SkChunk<NT>& c, f4 (&acc)[NT]) {
+template <int NT, int BMODE>
+__device__ __forceinline__ void sk_mfma(const SkChunk<NT>& c, f4 (&acc)[NT], int r, int g) {
+    if constexpr (BMODE == SK_X8) {
+        // lane (r, g) takes column r % 8 at k = 32 chunk + 4g (+16) from the lane that
+        // loaded it. MFMA rows 8..15 get copies of rows 0..7: they only reach output
+        // columns 8..15, which do not exist here and are never stored.
+        const int src0 = 4 * (8 * (r & 7) + g), src1 = src0 + 16;
+        // (the whole vector is cast: clang's __builtin_bit_cast of one element of a
+        // vector type reads element 0 whatever the index)
+        const i4 xi = __builtin_bit_cast(i4, c.x0[0]);
+        f4 a0, a1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            a0[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src0, xi[e]));
+            a1[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src1, xi[e]));
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[s], c.w0[s], acc[0], 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[s], c.w1[s], acc[0], 0, 0, 0);
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
@@ -368,7 +407,7 @@ template <int NT, int AHEAD, int BMODE>
 __global__ __launch_bounds__(SK_WAVES * 64) void k_mm_skinny(SkArgs p) {
     __shared__ float red[SK_WAVES * NT * 4 * 64];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches and offsets
     const int r = lane & 15, g = lane >> 4;
 
     const int64_t rb = blockIdx.x % p.row_blocks;
@@ -403,12 +442,15 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_mm_skinny(SkArgs p) {
     for (; n0 + AHEAD < mine; n0 += AHEAD) {
 #pragma unroll
         for (int u = 0; u < AHEAD; ++u) {
-            sk_mfma<NT>(buf[u], acc);
+            sk_mfma<NT, BMODE>(buf[u], acc, r, g);
             sk_load<NT, BMODE>(buf[u], rw, rx, wrow_off, p, wave, n0 + AHEAD + u, mine, g, r, rot);
+            // with the 8-column X loads the scheduler otherwise sinks the whole
+            // batch of refills below the last chunk's wait (1 us slower)
+            if constexpr (BMODE == SK_X8) __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
-    for (int u = 0; u < AHEAD; ++u) sk_mfma<NT>(buf[u], acc);
+    for (int u = 0; u < AHEAD; ++u) sk_mfma<NT, BMODE>(buf[u], acc, r, g);
 
     // partial sums of every wave, then the sum over waves in wave order
 #pragma unroll
@@ -431,7 +473,10 @@ template <int NT, int AHEAD>
 int launch_skinny_nt(SkArgs& p, int bmode, int64_t planes, hipStream_t stream) {
     const int64_t grid = p.row_blocks * planes;
     if (grid > 0x7FFFFFFF) return fail(TRC_HIP_E_SHAPE, "mul_mat: %lld workgroups exceed one launch", (long long) grid);
-    if (bmode == K_CONTIG) {
+    if (NT == 1 && bmode == K_CONTIG && p.N > 4 && p.N <= 8) {
+        // 5..8 columns: X in full lines (at 4 or fewer the 16-column loads are as fast)
+        hipLaunchKernelGGL((k_mm_skinny<1, AHEAD, SK_X8>), dim3((unsigned) grid), dim3(SK_WAVES * 64), 0, stream, p);
+    } else if (bmode == K_CONTIG) {
         hipLaunchKernelGGL((k_mm_skinny<NT, AHEAD, K_CONTIG>), dim3((unsigned) grid), dim3(SK_WAVES * 64), 0, stream, p);
     } else {
         // element-by-element X loads hold more addresses: half as many chunks ahead
