@@ -331,10 +331,12 @@ def linear_step(H, synth, timer, steps, warmup):
     """One training step of configuration 3's Linear layer with bias and the loss
     L = sum(mul(y, g)): the kernels HipDevice::graph_compute runs for the graph
     the reference's autograd builds (src/core/trc_autograd.cpp: graph_reset's
-    fills, then mul_mat, add, mul, sum, repeat, mul, repeat_back, acc, the
-    transposed mul_mat of dW^T, cont, acc, the transposed mul_mat of dX, acc), in
-    that order through the C ABI on one stream. Reported per step, with the
-    products' share."""
+    fills, then mul_mat, add, mul, sum, repeat, mul, repeat_back, acc, dW, the
+    transposed mul_mat of dX, acc), in that order through the C ABI on one
+    stream. dW's chain (the transposed product dW^T, its transpose, cont and the
+    acc into W's accumulator) runs as graph_compute fuses it: one product
+    mul_mat(X^T, dY^T) added into the accumulator (trc_hip_mul_mat_acc_f32).
+    Reported per step, with the products' share."""
     K = M = 4096
     T = 512
     f4 = 4
@@ -355,7 +357,7 @@ def linear_step(H, synth, timer, steps, warmup):
     bd = buf("b", M).upload(synth.normal(synth.config_seed(3, 3), M))
     Gd = buf("G", M * T).upload(synth.normal(synth.config_seed(3, 2), M * T, 0.0, 1e-2))
     for name, nf in (("MM", M * T), ("Y", M * T), ("YG", M * T), ("L", 1), ("dL", 1), ("R", M * T), ("DY", M * T),
-                     ("DB", M), ("DWt", M * K), ("DWc", K * M), ("DX", K * T), ("gW", K * M), ("gX", K * T),
+                     ("DB", M), ("DX", K * T), ("gW", K * M), ("gX", K * T),
                      ("gb", M)):
         buf(name, nf)
 
@@ -368,9 +370,7 @@ def linear_step(H, synth, timer, steps, warmup):
     DB, gb = t("DB", [M, 1, 1, 1]), t("gb", [M, 1, 1, 1])
     DYt = t("DY", [T, M, 1, 1], [M * f4, f4, M * T * f4, M * T * f4])
     Xt = t("X", [T, K, 1, 1], [K * f4, f4, K * T * f4, K * T * f4])
-    DWt = t("DWt", [M, K, 1, 1])
-    DWt_t = t("DWt", [K, M, 1, 1], [M * f4, f4, M * K * f4, M * K * f4])
-    DWc, gW = t("DWc", [K, M, 1, 1]), t("gW", [K, M, 1, 1])
+    gW = t("gW", [K, M, 1, 1])
     Wt = t("W", [M, K, 1, 1], [K * f4, f4, K * M * f4, K * M * f4])
     DX, gX = t("DX", [K, T, 1, 1]), t("gX", [K, T, 1, 1])
 
@@ -390,23 +390,22 @@ def linear_step(H, synth, timer, steps, warmup):
         H.mul_f32(R, G, DY, s)
         H.repeat_back_f32(DY, DB, s)
         H.acc_f32(gb, DB, gb, M * f4, M * f4, M * f4, 0, True, s)
-        H.mul_mat_f32(DYt, Xt, DWt, s)
-        H.cpy(DWt_t, DWc, s)
-        H.acc_f32(gW, DWc, gW, K * f4, K * M * f4, K * M * f4, 0, True, s)
+        H.mul_mat_acc_f32(Xt, DYt, gW, s)
         H.mul_mat_f32(Wt, DY, DX, s)
         H.acc_f32(gX, DX, gX, K * f4, K * T * f4, K * T * f4, 0, True, s)
 
     ms, mode = timer.run(step, steps, warmup)
     prods = {}
-    for name, (a, bb, d) in {"fwd": (W, X, MM), "dW^T": (DYt, Xt, DWt), "dX": (Wt, DY, DX)}.items():
-        pm, _ = timer.run(lambda i, s, a=a, bb=bb, d=d: H.mul_mat_f32(a, bb, d, s), steps, warmup)
+    for name, (a, bb, d, fn) in {"fwd": (W, X, MM, H.mul_mat_f32), "dW (added into its accumulator)":
+                                 (Xt, DYt, gW, H.mul_mat_acc_f32), "dX": (Wt, DY, DX, H.mul_mat_f32)}.items():
+        pm, _ = timer.run(lambda i, s, a=a, bb=bb, d=d, fn=fn: fn(a, bb, d, s), steps, warmup)
         prods[name] = round(pm * 1e3, 2)
     for v in bufs.values():
         v.free()
     fl = 3 * 2.0 * K * M * T
     return {"us": ms * 1e3, "products_us": prods, "products_sum_us": round(sum(prods.values()), 2),
             "other_kernels_us": round(ms * 1e3 - sum(prods.values()), 2), "TFLOP/s": fl / (ms * 1e-3) / 1e12,
-            "frac_mfma": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFS, "timing": mode, "kernel_launches": 17}
+            "frac_mfma": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFS, "timing": mode, "kernel_launches": 15}
 
 
 def mul_mat_config0(H, synth, timer, N, steps, warmup):

@@ -147,6 +147,19 @@ int trc_hip_dequant(int type, const void* blocks, int64_t n_blocks, float* dst, 
 int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b,
                         const trc_hip_tensor* dst, void* stream);
 
+/* dst += mul_mat(a, b): each element of the product is summed as
+ * trc_hip_mul_mat_f32 sums it (K is never split in parts here), then added to
+ * dst with one float add, the add OP_ACC makes (compute_acc,
+ * src/backends/cpu/trc_cpu_ops.cpp:954-999). No single reference op: it serves
+ * the fusion, in the plugin's graph_compute, of the chain autograd builds for a
+ * matrix gradient, mul_mat -> transpose -> cont -> inplace acc into the
+ * parameter's accumulator (src/core/trc_autograd.cpp:487-503 and
+ * grad_accumulate_inplace :58-77), computed as
+ * cont(transpose(mul_mat(x, y))) = mul_mat(y, x) added into the accumulator.
+ * Same argument rules as trc_hip_mul_mat_f32. */
+int trc_hip_mul_mat_acc_f32(const trc_hip_tensor* a, const trc_hip_tensor* b,
+                            const trc_hip_tensor* dst, void* stream);
+
 /* Fused quantized matvec / skinny GEMM: y = mul_mat(W, x) with W quantized.
  *   W : `type` blocks, ne = [K, M]; row m starts at wq + m*nb1_w bytes
  *       (2-byte aligned rows; 4-byte for Q4_1/Q5_1)

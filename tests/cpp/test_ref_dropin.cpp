@@ -274,6 +274,14 @@ void linear_full(Device* hip, int64_t K, int64_t M, int64_t T) {
     const double e_y = row_l2(y.data(), y_ref.data(), M, T), e_dw = row_l2(dW.data(), dW_ref.data(), K, M),
                  e_dx = row_l2(dX.data(), dX_ref.data(), K, T);
     std::printf("  row-L2 error vs oracle: y %.2e, dW %.2e, dX %.2e (bar 1e-4)\n", e_y, e_dw, e_dx);
+    // FNV-1a over the bits of y, dW, dX and db: runs with and without the plugin's
+    // fusion of dW's chain must print the same digest
+    uint64_t digest = 1469598103934665603ull;
+    for (const std::vector<float>* v : {&y, &dW, &dX, &db}) {
+        const uint8_t* p = (const uint8_t*) v->data();
+        for (size_t i = 0; i < v->size() * sizeof(float); ++i) digest = (digest ^ p[i]) * 1099511628211ull;
+    }
+    std::printf("  result digest %016llx\n", (unsigned long long) digest);
     CHECK(e_y <= 1e-4 && e_dw <= 1e-4 && e_dx <= 1e-4, "y / dW / dX beyond 1e-4");
     CHECK(same_bits(db.data(), db_ref.data(), db.size()), "db is not bit-identical to the oracle's repeat_back");
     CHECK(same_bits(L.data(), &L_ref, 1), "loss %.9g is not bit-identical to the oracle's sum(mul(y, g)) %.9g", L[0],

@@ -337,3 +337,67 @@ def test_few_columns_shapes(hip, shape, layout):
         B = rng.standard_normal((b3 * a3, b2 * a2, N, K + 1)).astype(np.float32)
         got, want = run_views(A, lambda x: x, B, lambda x: x[..., 1:])
     assert O.row_l2_error(got, want) <= TOL
+
+
+# ---------------------------------------------------------------- dst += mul_mat (trc_hip_mul_mat_acc_f32)
+
+def _acc_run(A, a_view_fn, B, b_view_fn, D0):
+    """GPU d0 + mul_mat(a, b) through the accumulate entry, and mul_mat(a, b) alone."""
+    da, db, dd = Dev(A), Dev(B), Dev(D0)
+    av, bv = a_view_fn(da.base), b_view_fn(db.base)
+    H.mul_mat_acc_f32(da.tensor(av), db.tensor(bv), dd.tensor())
+    H.sync()
+    got = dd.read()
+    mm = gpu_mul_mat(da, av, db, bv)
+    for d in (da, db, dd):
+        d.free()
+    return got, mm, av, bv
+
+
+@pytest.mark.parametrize("shape", [
+    # (K, M, N, a transposed, b transposed): the gradient of configuration 3's weight as
+    # the plugin fuses it (mul_mat(X^T, dY^T) into W's accumulator), smaller transposed
+    # products, and the few-column kernel
+    (512, 4096, 4096, True, True), (128, 1024, 768, True, True), (300, 130, 70, False, True),
+    (4096, 4096, 8, False, False), (1000, 77, 7, False, False), (96, 48, 40, True, False),
+])
+def test_mul_mat_acc_adds_the_product(hip, shape):
+    """Each element gets the product's float sum, then one float add into dst: the
+    result equals numpy float32 d0 + (the GPU's mul_mat of the same operands) bit for
+    bit, on shapes whose plain product keeps K whole, as these do."""
+    K, M, N, at, bt = shape
+    announce(f"mul_mat_acc K={K} M={M} N={N} a{'T' if at else ''} b{'T' if bt else ''}")
+    A = synth.normal(900 + K, K * M).reshape(1, 1, K, M) if at else synth.normal(900 + K, K * M).reshape(1, 1, M, K)
+    B = synth.normal(901 + N, K * N).reshape(1, 1, K, N) if bt else synth.normal(901 + N, K * N).reshape(1, 1, N, K)
+    D0 = synth.normal(902 + M, M * N).reshape(1, 1, N, M)
+    got, mm, av, bv = _acc_run(A, t01 if at else (lambda x: x), B, t01 if bt else (lambda x: x), D0)
+    assert np.array_equal(got.view(np.uint32), (D0 + mm).view(np.uint32))
+    if K * M * N <= 64 << 20:
+        assert O.row_l2_error(mm, O.mul_mat(av, bv, threads=8)) <= TOL
+
+
+def test_mul_mat_acc_keeps_k_whole(hip):
+    """Configuration 3's forward shape, whose plain product sums K in two parts into
+    a cleared dst: added into dst it keeps K whole (d + a + b would round differently
+    from d + (a + b)), and is checked against d0 + the oracle's product."""
+    announce("mul_mat_acc configuration 3 forward shape")
+    K, M, N = 4096, 4096, 512
+    W = synth.normal(910, K * M).reshape(1, 1, M, K)
+    X = synth.normal(911, K * N).reshape(1, 1, N, K)
+    D0 = synth.normal(912, M * N).reshape(1, 1, N, M)
+    got, _, av, bv = _acc_run(W, lambda x: x, X, lambda x: x, D0)
+    cols = np.arange(0, N, 37)
+    want = D0[:, :, cols, :] + O.mul_mat(av, np.ascontiguousarray(bv[:, :, cols, :]), threads=8)
+    assert O.row_l2_error(got[:, :, cols, :], want) <= TOL
+    again, _, _, _ = _acc_run(W, lambda x: x, X, lambda x: x, D0)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
+def test_mul_mat_acc_rejects_overlap(hip):
+    buf = empty((1, 1, 8, 8))
+    b3 = empty((1, 1, 6, 8))
+    with pytest.raises(H.HipError) as e:
+        H.mul_mat_acc_f32(buf.tensor(), b3.tensor(), H.tensor(buf.ptr + 16, [8, 6, 1, 1], H.contiguous_nb([8, 6, 1, 1])))
+    assert e.value.code == H.E_SHAPE
+    for t in (buf, b3):
+        t.free()

@@ -9,6 +9,7 @@ through the reference's gguf_load_tensor and through hip_gguf_load_tensor.
 Bars (written in the program): y, dW, dX within 1e-4 row-L2 of the oracle; db,
 the loss and the dequantized weights bit for bit; small graphs within the
 reference's conformance tolerance of its own CPU device."""
+import os
 import subprocess
 
 import pytest
@@ -40,3 +41,16 @@ def test_linear_autograd_and_gguf_on_the_reference_core(hip, tmp_path):
     print(r.stderr)
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-2000:]
     assert "ALL PASSED" in r.stdout
+    fused = [l for l in r.stdout.splitlines() if "result digest" in l]
+    assert len(fused) == 1
+
+    # The same program with the plugin's fusion of dW's chain (mul_mat -> transpose
+    # -> cont -> acc into W's accumulator, run as one product added into it) turned
+    # off: every check passes node by node too, and y, dW, dX and db are the same bits.
+    announce("the same, dW's chain node by node (TRC_HIP_NO_FUSION=1)")
+    r2 = subprocess.run([str(BIN), str(tmp_path / "cfg0b.gguf")], capture_output=True, text=True, timeout=600,
+                        cwd=tmp_path, env={**os.environ, "TRC_HIP_NO_FUSION": "1"})
+    print(r2.stdout)
+    assert r2.returncode == 0, r2.stdout[-4000:] + r2.stderr[-2000:]
+    assert "ALL PASSED" in r2.stdout
+    assert [l for l in r2.stdout.splitlines() if "result digest" in l] == fused

@@ -244,7 +244,13 @@ public:
 
     bool graph_compute(Graph* graph) override {
         select();
-        for (Tensor* node : graph->nodes) compute(node);
+        const std::vector<Tensor*>& nodes = graph->nodes;
+        std::vector<char> done(nodes.size(), 0);
+        for (size_t i = 0; i < nodes.size(); ++i) {
+            if (done[i]) continue;
+            if (fuse_gradient_product(nodes, i, done)) continue;
+            compute(nodes[i]);
+        }
         check(trc_hip_sync(nullptr), "graph_compute");
         return true;
     }
@@ -294,6 +300,94 @@ private:
                      "graph_first_unsupported() before graph_compute()\n",
                      t->name, op_name(t->op), type_name(t->type));
         std::abort();
+    }
+
+    // Byte range [first, last + 1) a tensor or view covers in its HIP buffer
+    // ({0, 0} outside one): every stride counts, so transposed views are covered.
+    struct Span {
+        uintptr_t lo, hi;
+    };
+    static Span span_of(const Tensor* t) {
+        HipBuffer* b = hip_buffer_of(t);
+        if (b == nullptr) return {0, 0};
+        const uintptr_t lo = (uintptr_t) b->address(t);
+        const int64_t blck = type_blck_size(t->type);
+        size_t n = type_size(t->type);
+        n += (size_t) ((blck > 0 ? t->ne[0] / blck : t->ne[0]) - 1) * t->nb[0];
+        for (int d = 1; d < MAX_DIMS; ++d) n += (size_t) (t->ne[d] - 1) * t->nb[d];
+        return {lo, lo + n};
+    }
+    static bool overlap(Span a, Span b) { return a.lo < b.hi && b.lo < a.hi; }
+
+    // The one node after position `from` that reads t (nullptr if none or more
+    // than one), and its position.
+    static Tensor* only_reader(const std::vector<Tensor*>& nodes, size_t from, const Tensor* t, size_t* at) {
+        Tensor* found = nullptr;
+        for (size_t k = from + 1; k < nodes.size(); ++k) {
+            for (int s = 0; s < MAX_SRC; ++s) {
+                if (nodes[k]->src[s] != t) continue;
+                if (found != nullptr && found != nodes[k]) return nullptr;
+                found = nodes[k];
+                *at = k;
+            }
+        }
+        return found;
+    }
+
+    // The chain autograd builds for a matrix operand's gradient
+    // (src/core/trc_autograd.cpp:487-503, then grad_accumulate_inplace :58-77):
+    //   m = mul_mat(x, y); v = transpose(m) (a view); c = cont(v); acc(G, c, inplace)
+    // adds transpose(mul_mat(x, y)) = mul_mat(y, x) into the accumulator G, so it
+    // runs as one product added into G (trc_hip_mul_mat_acc_f32): no m, no
+    // transposed copy, no separate acc pass. Taken only when m, v and c have no
+    // other reader and no output flag, the acc covers all of G, and no node
+    // between the product and the acc touches G's bytes, so G receives the same
+    // float adds at the same point of its history. TRC_HIP_NO_FUSION=1 turns it
+    // off (the chain then runs node by node).
+    bool fuse_gradient_product(const std::vector<Tensor*>& nodes, size_t i, std::vector<char>& done) {
+        static const bool off = std::getenv("TRC_HIP_NO_FUSION") != nullptr &&
+                                std::strcmp(std::getenv("TRC_HIP_NO_FUSION"), "0") != 0;
+        Tensor* m = nodes[i];
+        if (off || m->op != OP_MUL_MAT) return false;
+        Tensor* x = m->src[0];
+        Tensor* y = m->src[1];
+        if (x->type != TYPE_F32 || y->type != TYPE_F32 || x->ne[2] != y->ne[2] || x->ne[3] != y->ne[3]) return false;
+        size_t iv = 0, ic = 0, ia = 0;
+        Tensor* v = only_reader(nodes, i, m, &iv);
+        // (transpose() is permute(a, 1, 0, 2, 3) in the reference's core)
+        if (v == nullptr || (v->op != OP_TRANSPOSE && v->op != OP_PERMUTE) || v->view_src != m ||
+            v->view_offs != 0 || v->ne[0] != m->ne[1] ||
+            v->ne[1] != m->ne[0] || v->nb[0] != m->nb[1] || v->nb[1] != m->nb[0] || v->ne[2] != m->ne[2] ||
+            v->ne[3] != m->ne[3] || v->nb[2] != m->nb[2] || v->nb[3] != m->nb[3])
+            return false;
+        Tensor* c = only_reader(nodes, iv, v, &ic);
+        if (c == nullptr || c->op != OP_CONT || c->src[0] != v || c->type != TYPE_F32 || !tensor_is_contiguous(c))
+            return false;
+        Tensor* a = only_reader(nodes, ic, c, &ia);
+        if (a == nullptr || a->op != OP_ACC || a->src[1] != c) return false;
+        Tensor* g = a->src[0];
+        const AccParams q = acc_params(a);
+        if (!q.inplace || q.offset != 0 || q.nb1 != c->nb[1] || q.nb2 != c->nb[2] || q.nb3 != c->nb[3] ||
+            g->type != TYPE_F32 || !tensor_is_contiguous(g))
+            return false;
+        for (int d = 0; d < MAX_DIMS; ++d)
+            if (g->ne[d] != c->ne[d]) return false;
+        for (const Tensor* t : {m, v, c})
+            if (t->flags & (TENSOR_FLAG_OUTPUT | TENSOR_FLAG_LOSS | TENSOR_FLAG_PARAM)) return false;
+        const Span gs = span_of(g);
+        for (size_t k = i + 1; k < ia; ++k) {
+            if (k == iv || k == ic) continue;
+            const Tensor* n = nodes[k];
+            if (overlap(span_of(n), gs)) return false;
+            for (int s = 0; s < MAX_SRC; ++s)
+                if (n->src[s] != nullptr && overlap(span_of(n->src[s]), gs)) return false;
+        }
+        const trc_hip_tensor ty = describe(y, need_buffer(y));
+        const trc_hip_tensor tx = describe(x, need_buffer(x));
+        const trc_hip_tensor tg = describe(g, need_buffer(g));
+        check(trc_hip_mul_mat_acc_f32(&ty, &tx, &tg, nullptr), "mul_mat added into a gradient accumulator");
+        done[iv] = done[ic] = done[ia] = 1;
+        return true;
     }
 
     HipBuffer* need_buffer(const Tensor* t) const {

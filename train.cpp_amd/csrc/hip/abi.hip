@@ -199,35 +199,39 @@ int trc_hip_dequant(int type, const void* blocks, int64_t n_blocks, float* dst, 
     return launch_dequant(type, blocks, n_blocks, dst, (hipStream_t) stream);
 }
 
-int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst,
-                        void* stream) {
-    TRC_FORCED("trc_hip_mul_mat_f32");
+}  // extern "C"
+
+namespace {
+
+// The argument rules of both mul_mat entries; `who` names the entry in messages.
+int check_mul_mat_args(const char* who, const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst) {
     if (a == nullptr || b == nullptr || dst == nullptr) {
-        return fail(TRC_HIP_E_INVALID, "trc_hip_mul_mat_f32: NULL tensor");
+        return fail(TRC_HIP_E_INVALID, "%s: NULL tensor", who);
     }
     const trc_hip_tensor* ts[3] = {a, b, dst};
     for (const trc_hip_tensor* t : ts) {
-        if (t->type != TRC_HIP_TYPE_F32) return fail(TRC_HIP_E_INVALID, "trc_hip_mul_mat_f32: tensors must be F32");
+        if (t->type != TRC_HIP_TYPE_F32) return fail(TRC_HIP_E_INVALID, "%s: tensors must be F32", who);
         for (int i = 0; i < 4; ++i) {
-            if (t->ne[i] <= 0) return fail(TRC_HIP_E_SHAPE, "trc_hip_mul_mat_f32: ne[%d] = %lld", i, (long long) t->ne[i]);
-            if (t->nb[i] % 4 != 0) return fail(TRC_HIP_E_ALIGN, "trc_hip_mul_mat_f32: nb[%d] = %zu is not a multiple of 4", i, t->nb[i]);
+            if (t->ne[i] <= 0) return fail(TRC_HIP_E_SHAPE, "%s: ne[%d] = %lld", who, i, (long long) t->ne[i]);
+            if (t->nb[i] % 4 != 0) return fail(TRC_HIP_E_ALIGN, "%s: nb[%d] = %zu is not a multiple of 4", who, i, t->nb[i]);
         }
         if (t->data == nullptr || ((uintptr_t) t->data & 3u) != 0) {
-            return fail(TRC_HIP_E_ALIGN, "trc_hip_mul_mat_f32: data must be non-NULL and 4-byte aligned");
+            return fail(TRC_HIP_E_ALIGN, "%s: data must be non-NULL and 4-byte aligned", who);
         }
     }
     // ggml_can_mul_mat (src/ops/trc_ops.cpp:369-375) and the output shape (:380).
     if (a->ne[0] != b->ne[0] || b->ne[2] % a->ne[2] != 0 || b->ne[3] % a->ne[3] != 0 ||
         dst->ne[0] != a->ne[1] || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] || dst->ne[3] != b->ne[3]) {
         return fail(TRC_HIP_E_SHAPE,
-                    "trc_hip_mul_mat_f32: shapes a[%lld,%lld,%lld,%lld] b[%lld,%lld,%lld,%lld] dst[%lld,%lld,%lld,%lld] "
+                    "%s: shapes a[%lld,%lld,%lld,%lld] b[%lld,%lld,%lld,%lld] dst[%lld,%lld,%lld,%lld] "
                     "are not a mul_mat",
-                    (long long) a->ne[0], (long long) a->ne[1], (long long) a->ne[2], (long long) a->ne[3],
+                    who, (long long) a->ne[0], (long long) a->ne[1], (long long) a->ne[2], (long long) a->ne[3],
                     (long long) b->ne[0], (long long) b->ne[1], (long long) b->ne[2], (long long) b->ne[3],
                     (long long) dst->ne[0], (long long) dst->ne[1], (long long) dst->ne[2], (long long) dst->ne[3]);
     }
-    // dst may be cleared before the sums are added into it, so it must not
-    // share bytes with an operand (compared by the byte spans the views cover)
+    // dst may be cleared before the sums are added into it (and is read and
+    // written while the operands are read), so it must not share bytes with an
+    // operand (compared by the byte spans the views cover)
     auto span_end = [](const trc_hip_tensor* t) {
         uintptr_t e = (uintptr_t) t->data + 4;
         for (int i = 0; i < 4; ++i) e += (uintptr_t) (t->ne[i] - 1) * t->nb[i];
@@ -235,10 +239,30 @@ int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const 
     };
     for (const trc_hip_tensor* t : {a, b}) {
         if ((uintptr_t) dst->data < span_end(t) && (uintptr_t) t->data < span_end(dst)) {
-            return fail(TRC_HIP_E_SHAPE, "trc_hip_mul_mat_f32: dst overlaps an operand");
+            return fail(TRC_HIP_E_SHAPE, "%s: dst overlaps an operand", who);
         }
     }
+    return TRC_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst,
+                        void* stream) {
+    TRC_FORCED("trc_hip_mul_mat_f32");
+    const int rc = check_mul_mat_args("trc_hip_mul_mat_f32", a, b, dst);
+    if (rc != TRC_HIP_OK) return rc;
     return launch_mul_mat_f32(*a, *b, *dst, (hipStream_t) stream);
+}
+
+int trc_hip_mul_mat_acc_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_hip_tensor* dst,
+                            void* stream) {
+    TRC_FORCED("trc_hip_mul_mat_acc_f32");
+    const int rc = check_mul_mat_args("trc_hip_mul_mat_acc_f32", a, b, dst);
+    if (rc != TRC_HIP_OK) return rc;
+    return launch_mul_mat_f32(*a, *b, *dst, (hipStream_t) stream, true);
 }
 
 }  // extern "C"

@@ -44,8 +44,9 @@ int device_cus();
 // Kernel launchers (one per kernel family). They validate what the kernels
 // assume, enqueue on `stream` and return a trc_hip_status / hipError_t.
 int launch_dequant(int type, const void* blocks, int64_t n_blocks, float* dst, hipStream_t stream);
+// accumulate: dst += the product (each element's float sum, then one add)
 int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d,
-                       hipStream_t stream);
+                       hipStream_t stream, bool accumulate = false);
 // Where the fp16 matrix-core path of the fused matvec keeps x's planes and
 // scales (qmm.hip): a workspace per (device, stream), allocated by the first
 // such call on that stream (trc_hip_qmatvec), or the fixed device array of the

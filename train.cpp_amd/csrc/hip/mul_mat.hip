@@ -143,10 +143,12 @@ struct SlabLoader {
 };
 
 // SPLIT: parts of K (1, or 2 summed into a cleared dst with atomic adds).
-template <int WI, int WJ, int TI, int TJ, int BK, int AMODE, int BMODE, int SPLIT>
+// ACC: dst += the product (K in one part).
+template <int WI, int WJ, int TI, int TJ, int BK, int AMODE, int BMODE, int SPLIT, bool ACC = false>
 __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
     constexpr int THREADS = WI * WJ * 64;
     static_assert(SPLIT == 1 || SPLIT == 2, "two parts at most keep the atomic sums deterministic");
+    static_assert(!ACC || SPLIT == 1, "d + a + b would round differently from d + (a + b)");
     constexpr int BM = WI * TI * 32;  // tile extent along i
     constexpr int BN = WJ * TJ * 32;  // tile extent along j
     using LA = SlabLoader<AMODE, BM, BK, THREADS>;
@@ -246,6 +248,24 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
         if (i >= p.M) continue;
 #pragma unroll
         for (int y = 0; y < TJ; ++y) {
+            if constexpr (ACC) {
+                // d + v, the float add acc would make with this product. All 16
+                // old values are read before any store: interleaved, each read
+                // would wait for the store before it (the compiler cannot tell
+                // the addresses apart), 64 round trips per lane.
+                float old[16];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t j = j0 + (wj * TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                    old[v] = j < p.N ? *(const float*) (d + i * p.d_nb0 + j * p.d_nb1) : 0.f;
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t j = j0 + (wj * TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                    if (j < p.N) *(float*) (d + i * p.d_nb0 + j * p.d_nb1) = old[v] + acc[x][y][v];
+                }
+                continue;
+            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t j = j0 + (wj * TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
@@ -308,6 +328,7 @@ struct SkArgs {
     int64_t row_blocks;  // ceil(M / 16)
     int64_t x_span;      // bytes from one X plane's first element to past its last
     int chunks;          // ceil(K / 32)
+    int accumulate;      // 1: dst += the product
 };
 
 constexpr int SK_WAVES = 16;
@@ -465,7 +486,10 @@ __global__ __launch_bounds__(SK_WAVES * 64) void k_mm_skinny(SkArgs p) {
         const int el = e & 63, tv = e >> 6;  // tv = 4t + v
         const int64_t j = 16 * (tv >> 2) + 4 * (el >> 4) + (tv & 3);
         const int64_t di = rb * 16 + (el & 15);
-        if (di < p.M && j < p.N) *(float*) (p.d + i2 * p.d_nb2 + i3 * p.d_nb3 + di * p.d_nb0 + j * p.d_nb1) = s;
+        if (di < p.M && j < p.N) {
+            float* dst = (float*) (p.d + i2 * p.d_nb2 + i3 * p.d_nb3 + di * p.d_nb0 + j * p.d_nb1);
+            *dst = p.accumulate ? *dst + s : s;
+        }
     }
 }
 
@@ -497,7 +521,7 @@ int pick_mode(const trc_hip_tensor& t, int64_t rows) {
     return GENERIC;
 }
 
-template <int WI, int WJ, int TI, int TJ, int BK, int AM, int BMO, int SPLIT>
+template <int WI, int WJ, int TI, int TJ, int BK, int AM, int BMO, int SPLIT, bool ACC>
 int launch_cfg(MMArgs& p, int64_t planes, hipStream_t stream) {
     constexpr int BM = WI * TI * 32, BN = WJ * TJ * 32;
     p.tiles_i = (p.M + BM - 1) / BM;
@@ -505,15 +529,15 @@ int launch_cfg(MMArgs& p, int64_t planes, hipStream_t stream) {
     const int64_t grid = p.tiles_i * p.tiles_j * planes * SPLIT;
     if (grid > 0x7FFFFFFF) return fail(TRC_HIP_E_SHAPE, "mul_mat: %lld workgroups exceed one launch", (long long) grid);
     p.xcd_planes = planes % 8 == 0 ? 1 : 0;
-    hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, BK, AM, BMO, SPLIT>), dim3((unsigned) grid), dim3(WI * WJ * 64), 0,
-                       stream, p);
+    hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, BK, AM, BMO, SPLIT, ACC>), dim3((unsigned) grid),
+                       dim3(WI * WJ * 64), 0, stream, p);
     return check_launch("mul_mat_f32");
 }
 
-template <int WI, int WJ, int TI, int TJ, int BK, int SPLIT>
+template <int WI, int WJ, int TI, int TJ, int BK, int SPLIT, bool ACC = false>
 int dispatch_modes(MMArgs& p, int am, int bm, int64_t planes, hipStream_t s) {
 #define TRC_MM_CASE(A, B) \
-    if (am == A && bm == B) return launch_cfg<WI, WJ, TI, TJ, BK, A, B, SPLIT>(p, planes, s);
+    if (am == A && bm == B) return launch_cfg<WI, WJ, TI, TJ, BK, A, B, SPLIT, ACC>(p, planes, s);
     TRC_MM_CASE(K_CONTIG, K_CONTIG)
     TRC_MM_CASE(K_CONTIG, R_CONTIG)
     TRC_MM_CASE(K_CONTIG, GENERIC)
@@ -530,7 +554,7 @@ int dispatch_modes(MMArgs& p, int am, int bm, int64_t planes, hipStream_t s) {
 }  // namespace
 
 int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d,
-                       hipStream_t stream) {
+                       hipStream_t stream, bool accumulate) {
     MMArgs p;
     p.a = (const uint8_t*) a.data;
     p.b = (const uint8_t*) b.data;
@@ -559,6 +583,7 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
         s.a_nb1 = p.a_nb1; s.a_nb2 = p.a_nb2; s.a_nb3 = p.a_nb3; s.a_ne2 = p.a_ne2; s.a_ne3 = p.a_ne3;
         s.b_nb0 = p.b_nb0; s.b_nb1 = p.b_nb1; s.b_nb2 = p.b_nb2; s.b_nb3 = p.b_nb3; s.b_ne2 = p.b_ne2;
         s.d_nb0 = p.d_nb0; s.d_nb1 = p.d_nb1; s.d_nb2 = p.d_nb2; s.d_nb3 = p.d_nb3;
+        s.accumulate = accumulate ? 1 : 0;
         s.row_blocks = (p.M + 15) / 16;
         s.x_span = x_span;
         s.chunks = (int) ((p.K + 31) / 32);
@@ -574,6 +599,11 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
     // between half and two tiles per CU and a long K, large tiles with K in two
     // parts (into a cleared, contiguous dst); otherwise 64x64 tiles.
     const int64_t big_tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128) * planes;
+    if (accumulate) {
+        // K stays in one part: the large tiles when they fill the CUs twice, else 64 x 64
+        if (big_tiles >= 512) return dispatch_modes<2, 2, 2, 2, 16, 1, true>(p, am, bm, planes, stream);
+        return dispatch_modes<2, 2, 1, 1, 32, 1, true>(p, am, bm, planes, stream);
+    }
     if (big_tiles >= 512) return dispatch_modes<2, 2, 2, 2, 16, 1>(p, am, bm, planes, stream);
     const bool dense_dst = p.d_nb0 == 4 && p.d_nb1 == 4 * p.M && p.d_nb2 == p.d_nb1 * p.N &&
                            p.d_nb3 == p.d_nb2 * b.ne[2];

@@ -25,6 +25,7 @@ EXPORTS = (
     "trc_hip_fill_f32", "trc_hip_dequant", "trc_hip_mul_mat_f32", "trc_hip_qmatvec", "trc_hip_cpy",
     "trc_hip_add_f32", "trc_hip_acc_f32", "trc_hip_repeat_back_f32", "trc_hip_qmatvec_noalloc",
     "trc_hip_mul_f32", "trc_hip_repeat_f32", "trc_hip_sum_f32", "trc_hip_qmatvec_release_stream",
+    "trc_hip_mul_mat_acc_f32",
 )
 
 
@@ -92,6 +93,7 @@ def load() -> C.CDLL:
         "trc_hip_fill_f32": ([P, F, I64, P], I),
         "trc_hip_dequant": ([I, P, I64, P, P], I),
         "trc_hip_mul_mat_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
+        "trc_hip_mul_mat_acc_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_qmatvec": ([I, P, I64, I64, SZ, P, I64, SZ, P, SZ, P], I),
         "trc_hip_qmatvec_noalloc": ([I, P, I64, I64, SZ, P, I64, SZ, P, SZ, P], I),
         "trc_hip_qmatvec_release_stream": ([P], I),
@@ -144,6 +146,11 @@ def dequant(type_: int, blocks_ptr: int, n_blocks: int, dst_ptr: int, stream: in
 
 def mul_mat_f32(a: Tensor, b: Tensor, d: Tensor, stream: int | None = None) -> None:
     check(load().trc_hip_mul_mat_f32(C.byref(a), C.byref(b), C.byref(d), stream))
+
+
+def mul_mat_acc_f32(a: Tensor, b: Tensor, d: Tensor, stream: int | None = None) -> None:
+    """d += mul_mat(a, b) (trc_hip_mul_mat_acc_f32)."""
+    check(load().trc_hip_mul_mat_acc_f32(C.byref(a), C.byref(b), C.byref(d), stream))
 
 
 def qmatvec(type_: int, w_ptr: int, K: int, M: int, nb1_w: int, x_ptr: int, N: int, nb1_x: int,
