@@ -156,7 +156,8 @@ int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b,
  * parameter's accumulator (src/core/trc_autograd.cpp:487-503 and
  * grad_accumulate_inplace :58-77), computed as
  * cont(transpose(mul_mat(x, y))) = mul_mat(y, x) added into the accumulator.
- * Same argument rules as trc_hip_mul_mat_f32. */
+ * Same argument rules as trc_hip_mul_mat_f32; one dst plane (ne0 x ne1) may span
+ * at most 2 GiB (TRC_HIP_E_SHAPE beyond). */
 int trc_hip_mul_mat_acc_f32(const trc_hip_tensor* a, const trc_hip_tensor* b,
                             const trc_hip_tensor* dst, void* stream);
 

@@ -74,6 +74,11 @@ def test_forced_error_hook_on_cpu():
     # before any device work, so the fake addresses are never dereferenced
     "H.check(H.load().trc_hip_qmatvec(2, 0x100000, 64, 4, 36, 0x200000, 1, 256, 0x100040, 16, None))",
     "H.check(H.load().trc_hip_qmatvec(2, 0x100000, 64, 4, 36, 0x200000, 2, 256, 0x2000f0, 16, None))",
+    # dst += mul_mat with one dst plane of 65536 x 32768 floats (8 GiB): over the
+    # 2 GiB the accumulate kernels address, refused before any device work
+    "H.mul_mat_acc_f32(H.tensor(0x100000, [4, 65536, 1, 1], H.contiguous_nb([4, 65536, 1, 1])), "
+    "H.tensor(0x200000, [4, 32768, 1, 1], H.contiguous_nb([4, 32768, 1, 1])), "
+    "H.tensor(0x1000000000, [65536, 32768, 1, 1], H.contiguous_nb([65536, 32768, 1, 1])))",
 ])
 def test_argument_validation_precedes_device_work(bad):
     code = "import conftest\nfrom traincpp_amd import hip as H\ntry:\n    " + bad + \

@@ -372,6 +372,7 @@ private:
             return false;
         for (int d = 0; d < MAX_DIMS; ++d)
             if (g->ne[d] != c->ne[d]) return false;
+        if ((uint64_t) g->ne[0] * (uint64_t) g->ne[1] * sizeof(float) >= (1ull << 31)) return false;  // one plane <= 2 GiB
         for (const Tensor* t : {m, v, c})
             if (t->flags & (TENSOR_FLAG_OUTPUT | TENSOR_FLAG_LOSS | TENSOR_FLAG_PARAM)) return false;
         const Span gs = span_of(g);

@@ -262,6 +262,12 @@ int trc_hip_mul_mat_acc_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, co
     TRC_FORCED("trc_hip_mul_mat_acc_f32");
     const int rc = check_mul_mat_args("trc_hip_mul_mat_acc_f32", a, b, dst);
     if (rc != TRC_HIP_OK) return rc;
+    // the kernels address one dst plane through 32-bit buffer offsets
+    const uint64_t plane = (uint64_t) (dst->ne[0] - 1) * dst->nb[0] + (uint64_t) (dst->ne[1] - 1) * dst->nb[1] + 4;
+    if (plane >= (1ull << 31)) {
+        return fail(TRC_HIP_E_SHAPE, "trc_hip_mul_mat_acc_f32: a dst plane spans %llu bytes (2 GiB at most)",
+                    (unsigned long long) plane);
+    }
     return launch_mul_mat_f32(*a, *b, *dst, (hipStream_t) stream, true);
 }
 

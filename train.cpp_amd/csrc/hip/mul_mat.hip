@@ -55,7 +55,11 @@ struct MMArgs {
     int64_t d_nb0, d_nb1, d_nb2, d_nb3;
     int64_t tiles_i, tiles_j;
     int xcd_planes;  // 1: planes % 8 == 0, tiles of plane p on XCD p % 8
+    int64_t d_span;  // bytes from a dst plane's first element to past its last
 };
+
+constexpr uint32_t MM_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
+constexpr uint32_t MM_OUT = 0x80000000u;         // an offset past the resource: loads read 0, stores drop
 
 // Loads a ROWS x BK slab (rows = i for src0, j for src1) of one operand into
 // registers, then stores it to LDS as lds[k * LD + row].
@@ -242,30 +246,67 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
 
     // Accumulator register v of lane l holds MFMA row 8*(v/4) + 4*(l/32) + v%4
     // (a j offset) and column l%32 (an i offset).
+    if constexpr (ACC) {
+        // d + v, the float add acc would make with this product, one 32 x 32
+        // block at a time, all 16 old values read before any store (interleaved,
+        // each read would wait for the store before it: the compiler cannot tell
+        // the addresses apart). Through a buffer resource over the dst plane
+        // (under 2 GiB, checked on the host) the 16 addresses are one lane offset
+        // plus uniform multiples of nb1, and rows or columns past dst get an
+        // offset past the resource (reads 0, stores dropped), so there is no
+        // branch and each block's accumulators are read only when it is stored.
+        const __amdgpu_buffer_rsrc_t rd =
+            __builtin_amdgcn_make_buffer_rsrc((void*) d, (short) 0, (int) p.d_span, MM_RSRC_WORD3);
+#pragma unroll
+        for (int x = 0; x < TI; ++x) {
+            const int64_t i = i0 + (wi * TI + x) * 32 + col;
+#pragma unroll
+            for (int y = 0; y < TJ; ++y) {
+                const int64_t jb = j0 + (wj * TJ + y) * 32 + 4 * half;
+                const uint32_t vo = i < p.M ? (uint32_t) (i * p.d_nb0 + jb * p.d_nb1) : MM_OUT;
+                float old[16];
+                if (j0 + BN <= p.N) {  // every column of the tile exists: one offset
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const uint32_t so = (uint32_t) ((8 * (v >> 2) + (v & 3)) * p.d_nb1);
+                        old[v] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, vo, so, 0));
+                    }
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const uint32_t so = (uint32_t) ((8 * (v >> 2) + (v & 3)) * p.d_nb1);
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, old[v] + acc[x][y][v]), rd,
+                                                              vo, so, 0);
+                    }
+                } else {  // the tile's last columns lie past dst: four at a time (fewer offsets held)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                        for (int v = 4 * q; v < 4 * q + 4; ++v) {
+                            const int c = 8 * (v >> 2) + (v & 3);
+                            old[v] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                   rd, jb + c < p.N ? vo : MM_OUT, (uint32_t) (c * p.d_nb1), 0));
+                        }
+#pragma unroll
+                        for (int v = 4 * q; v < 4 * q + 4; ++v) {
+                            const int c = 8 * (v >> 2) + (v & 3);
+                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, old[v] + acc[x][y][v]),
+                                                                  rd, jb + c < p.N ? vo : MM_OUT,
+                                                                  (uint32_t) (c * p.d_nb1), 0);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int x = 0; x < TI; ++x) {
         const int64_t i = i0 + (wi * TI + x) * 32 + col;
         if (i >= p.M) continue;
 #pragma unroll
         for (int y = 0; y < TJ; ++y) {
-            if constexpr (ACC) {
-                // d + v, the float add acc would make with this product. All 16
-                // old values are read before any store: interleaved, each read
-                // would wait for the store before it (the compiler cannot tell
-                // the addresses apart), 64 round trips per lane.
-                float old[16];
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t j = j0 + (wj * TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    old[v] = j < p.N ? *(const float*) (d + i * p.d_nb0 + j * p.d_nb1) : 0.f;
-                }
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t j = j0 + (wj * TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    if (j < p.N) *(float*) (d + i * p.d_nb0 + j * p.d_nb1) = old[v] + acc[x][y][v];
-                }
-                continue;
-            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t j = j0 + (wj * TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
@@ -529,6 +570,7 @@ int launch_cfg(MMArgs& p, int64_t planes, hipStream_t stream) {
     const int64_t grid = p.tiles_i * p.tiles_j * planes * SPLIT;
     if (grid > 0x7FFFFFFF) return fail(TRC_HIP_E_SHAPE, "mul_mat: %lld workgroups exceed one launch", (long long) grid);
     p.xcd_planes = planes % 8 == 0 ? 1 : 0;
+    p.d_span = (p.M - 1) * p.d_nb0 + (p.N - 1) * p.d_nb1 + 4;
     hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, BK, AM, BMO, SPLIT, ACC>), dim3((unsigned) grid),
                        dim3(WI * WJ * 64), 0, stream, p);
     return check_launch("mul_mat_f32");
