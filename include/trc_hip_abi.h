@@ -239,6 +239,20 @@ int trc_hip_mul_f32(const trc_hip_tensor* a, const trc_hip_tensor* b, const trc_
  * copy, bit-identical. */
 int trc_hip_repeat_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream);
 
+/* ggml sqr: dst = a * a element by element, dst with a's shape, any strides.
+ * OP_SQR (src/ops/trc_ops.cpp:75-77) as computed by compute_unary with fn_sqr
+ * (src/backends/cpu/trc_cpu_ops.cpp:86, 119-135): one float multiply per element,
+ * bit-identical. The square of a loss term, as in the reference's gradient tests
+ * of mul_mat (tests/test_grad.cpp:343-373). F32 only. */
+int trc_hip_sqr_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream);
+
+/* ggml scale: dst = a * s element by element, dst with a's shape, any strides.
+ * OP_SCALE (src/ops/trc_ops.cpp:107-115, s in op_params) as computed by
+ * compute_scale (src/backends/cpu/trc_cpu_ops.cpp:140-150): one float multiply,
+ * bit-identical. Autograd builds it for sqr's gradient, 2 * (x * grad)
+ * (src/core/trc_autograd.cpp:288-292). F32 only. */
+int trc_hip_scale_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, float s, void* stream);
+
 /* ggml sum: the one element of dst = the sum of every element of a (any strides).
  * OP_SUM (src/ops/trc_ops.cpp:214-221) as computed by compute_sum
  * (src/backends/cpu/trc_cpu_ops.cpp:302-315, row_sum_f32 :284-300): each row

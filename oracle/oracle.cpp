@@ -329,6 +329,29 @@ int orc_mul(const void* a, const int64_t a_ne[4], const size_t a_nb[4],
     return binary_f32(a, a_ne, a_nb, b, b_ne, b_nb, d, d_ne, d_nb, [](float x, float y) { return x * y; });
 }
 
+// compute_unary with fn_sqr (src/backends/cpu/trc_cpu_ops.cpp:86, 119-135) and
+// compute_scale (:140-150): dst element i (linear order) from a's element i,
+// one float multiply each.
+static int unary_f32(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const size_t d_nb[4],
+                     int sqr, float s) {
+    const uint8_t* pa = (const uint8_t*) a;
+    uint8_t* pd = (uint8_t*) d;
+    const int64_t n = nelem(a_ne);
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = *(const float*) (pa + lin_offset(a_ne, a_nb, i));
+        *(float*) (pd + lin_offset(a_ne, d_nb, i)) = sqr ? v * v : v * s;
+    }
+    return 0;
+}
+
+int orc_sqr(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const size_t d_nb[4]) {
+    return unary_f32(a, a_ne, a_nb, d, d_nb, 1, 0.f);
+}
+
+int orc_scale(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const size_t d_nb[4], float s) {
+    return unary_f32(a, a_ne, a_nb, d, d_nb, 0, s);
+}
+
 // compute_sum (src/backends/cpu/trc_cpu_ops.cpp:302-315): rows in the order i3,
 // i2, i1; each row summed in double from 0 along i0 (row_sum_f32 :284-300); the
 // row sums added in double; one rounding to float.

@@ -48,6 +48,10 @@
  *   orc_repeat         - tests/test_ops.cpp:795-815, the PyTorch golden
  *                        tests/golden/repeat_*, numpy's tile, and the reference's
  *                        compute_repeat (oracle/_ref), bit for bit.
+ *   orc_sqr, orc_scale - numpy's float32 x * x and x * s (finite, signed zeros,
+ *                        subnormals, inf and NaN inputs) and the reference's
+ *                        compute_unary / compute_scale (oracle/_ref) on strided
+ *                        views, bit for bit.
  */
 #pragma once
 
@@ -133,6 +137,12 @@ int orc_sum(const void* a, const int64_t a_ne[4], const size_t a_nb[4], float* o
  * src/backends/cpu/trc_cpu_ops.cpp:913-928). */
 int orc_repeat(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const int64_t d_ne[4],
                const size_t d_nb[4]);
+
+/* sqr: d = a * a; scale: d = a * s. d has a's shape (own strides d_nb)
+ * (src/ops/trc_ops.cpp:75-77, 107-115; compute_unary / compute_scale
+ * src/backends/cpu/trc_cpu_ops.cpp:86, 119-150). */
+int orc_sqr(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const size_t d_nb[4]);
+int orc_scale(const void* a, const int64_t a_ne[4], const size_t a_nb[4], void* d, const size_t d_nb[4], float s);
 
 /* splitmix64 stream (src/core/trc_rng.cpp:38-68). */
 uint64_t orc_rng_next_u64(uint64_t* state);

@@ -390,4 +390,25 @@ int ref_repeat(const float* a, const int64_t a_ne[4], const int pa[4], const int
     return ok ? 0 : -2;
 }
 
+// sqr(permute(a)) (sq != 0) or scale(permute(a), s) on the reference CPU device;
+// out contiguous with the permuted shape.
+int ref_unary(const float* a, const int64_t a_ne[4], const int pa[4], int sq, float s, float* out) {
+    Device* dev = device_cpu();
+    if (!dev) return -1;
+    Context* ctx = context_new(1 << 20);
+    Tensor* ta = new_tensor_4d(ctx, TYPE_F32, a_ne[0], a_ne[1], a_ne[2], a_ne[3]);
+    Tensor* va = permute(ctx, ta, pa[0], pa[1], pa[2], pa[3]);
+    Tensor* r = sq ? sqr(ctx, va) : scale(ctx, va, s);
+    Graph* g = graph_new(ctx);
+    graph_build_forward_expand(ctx, g, r);
+    Buffer* buf = buffer_alloc_ctx_tensors(ctx, dev->default_buffer_type());
+    tensor_set(ta, a, 0, tensor_nbytes(ta));
+    const bool ok = dev->graph_compute(g);
+    tensor_get(r, out, 0, tensor_nbytes(r));
+    buffer_free(buf);
+    graph_free(g);
+    context_free(ctx);
+    return ok ? 0 : -2;
+}
+
 }  // extern "C"

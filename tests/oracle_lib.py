@@ -56,6 +56,10 @@ def oracle() -> C.CDLL:
         lib.orc_sum.restype = I
         lib.orc_repeat.argtypes = [P, NE, NB, P, NE, NB]
         lib.orc_repeat.restype = I
+        lib.orc_sqr.argtypes = [P, NE, NB, P, NB]
+        lib.orc_sqr.restype = I
+        lib.orc_scale.argtypes = [P, NE, NB, P, NB, C.c_float]
+        lib.orc_scale.restype = I
         lib.orc_rng_next_u64.argtypes = [C.POINTER(C.c_uint64)]
         lib.orc_rng_next_u64.restype = C.c_uint64
         lib.orc_rng_uniform01.argtypes = [C.POINTER(C.c_uint64)]
@@ -94,6 +98,8 @@ def ref() -> C.CDLL:
         lib.ref_sum.restype = I
         lib.ref_repeat.argtypes = [P, NE, AX, NE, P]
         lib.ref_repeat.restype = I
+        lib.ref_unary.argtypes = [P, NE, AX, I, F, P]
+        lib.ref_unary.restype = I
         for n in ("ref_rng_next_u64", "ref_rng_uniform01"):
             getattr(lib, n).argtypes = [C.POINTER(C.c_uint64)]
         lib.ref_rng_next_u64.restype = C.c_uint64
@@ -278,6 +284,24 @@ def sum_all(a: np.ndarray) -> np.float32:
     return np.float32(out.value)
 
 
+def sqr(a: np.ndarray) -> np.ndarray:
+    """Oracle sqr of a (possibly strided) float32 view; contiguous result with a's shape."""
+    pa, ane, anb = base_ptr_and_meta(a)
+    out = np.zeros(ggml_shape(ane), dtype=np.float32)
+    _, _, dnb = base_ptr_and_meta(out)
+    assert oracle().orc_sqr(pa, NE(*ane), NB(*anb), out.ctypes.data, NB(*dnb)) == 0
+    return out
+
+
+def scale(a: np.ndarray, s: float) -> np.ndarray:
+    """Oracle scale (a * s) of a (possibly strided) float32 view; contiguous result."""
+    pa, ane, anb = base_ptr_and_meta(a)
+    out = np.zeros(ggml_shape(ane), dtype=np.float32)
+    _, _, dnb = base_ptr_and_meta(out)
+    assert oracle().orc_scale(pa, NE(*ane), NB(*anb), out.ctypes.data, NB(*dnb), s) == 0
+    return out
+
+
 def repeat(a: np.ndarray, d_ne) -> np.ndarray:
     """Oracle repeat of a (possibly strided) view to ggml shape d_ne; contiguous result."""
     pa, ane, anb = base_ptr_and_meta(a)
@@ -375,5 +399,15 @@ def ref_repeat(a_base: np.ndarray, pa, d_ne) -> np.ndarray:
     d_ne = list(d_ne) + [1] * (4 - len(d_ne))
     out = np.zeros(ggml_shape(d_ne), dtype=np.float32)
     rc = ref().ref_repeat(a_base.ctypes.data, NE(*ane), AX(*pa), NE(*d_ne), out.ctypes.data)
+    assert rc == 0, rc
+    return out
+
+
+def ref_unary(a_base: np.ndarray, pa, sq: bool, s: float = 0.0) -> np.ndarray:
+    """Reference library sqr(permute(A, pa)) or scale(permute(A, pa), s) on its CPU device."""
+    a_base = np.ascontiguousarray(a_base, dtype=np.float32)
+    ane = list(a_base.shape)[::-1] + [1] * (4 - a_base.ndim)
+    out = np.zeros(ggml_shape(_perm_ne(ane, pa)), dtype=np.float32)
+    rc = ref().ref_unary(a_base.ctypes.data, NE(*ane), AX(*pa), 1 if sq else 0, s, out.ctypes.data)
     assert rc == 0, rc
     return out

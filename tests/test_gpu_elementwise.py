@@ -307,3 +307,70 @@ def test_sum_order_and_strides_bitwise(hip):
     A = rng.standard_normal((6, 70, 50)).astype(np.float32)
     av = A.transpose(2, 0, 1)  # strided rows
     assert bits(gpu_sum(A, av)) == bits(O.sum_all(av))
+
+
+def gpu_unary(a_base, a_view, s=None):
+    """sqr (s None) or scale by s of a view of a_base on the device; contiguous result."""
+    da = Dev(a_base)
+    ne, _ = O.view_meta(a_view)
+    out = empty(O.ggml_shape(ne))
+    if s is None:
+        H.sqr_f32(da.tensor(a_view), out.tensor())
+    else:
+        H.scale_f32(da.tensor(a_view), out.tensor(), s)
+    H.sync()
+    r = out.read()
+    da.free()
+    out.free()
+    return r
+
+
+def _unary_specials():
+    """Values whose square or scaled product rounds, overflows, underflows to a
+    subnormal or zero, or carries a NaN or an infinity through."""
+    return np.array([0.0, -0.0, 1.0, -1.5, 3.4e38, -1.9e19, 1.9e19, 1.2e-38, 1.4e-45, -1e-23, 1e-20,
+                     np.inf, -np.inf, np.nan, 1.0000001, 3.0e-3, 7.7, -2.5e5], np.float32)
+
+
+@pytest.mark.parametrize("shape", [(3, 5, 7, 64), (4, 6, 33), (257,), (1, 1, 1, 1), (2, 3, 4100)])
+@pytest.mark.parametrize("s", [None, 2.0, -0.37, 1e-30])
+def test_sqr_and_scale_bitwise(hip, shape, s):
+    """Contiguous tensors: rows of a multiple of four floats take the kernel that
+    reads four floats per lane, the others the one-float kernel."""
+    announce(f"{'sqr' if s is None else f'scale {s}'} {shape}")
+    rng = np.random.default_rng(31)
+    a = (rng.standard_normal(shape) * 10.0 ** rng.integers(-20, 20, shape)).astype(np.float32)
+    want = O.sqr(a) if s is None else O.scale(a, s)
+    assert (bits(gpu_unary(a, a, s)) == bits(want)).all()
+
+
+@pytest.mark.parametrize("s", [None, 2.0, 1e-30, 1e30])
+def test_sqr_and_scale_special_values_bitwise(hip, s):
+    announce(f"{'sqr' if s is None else f'scale {s}'} specials")
+    sp = _unary_specials()
+    a = np.concatenate([sp, -sp, sp * np.float32(0.5)]).astype(np.float32)
+    a = np.tile(a, 8).reshape(6, 72)  # 72-float rows: the four-floats-per-lane kernel
+    want = O.sqr(a) if s is None else O.scale(a, s)
+    assert (bits(gpu_unary(a, a, s)) == bits(want)).all()
+    b = a[:, :71]  # rows cut to 71 floats: the one-float kernel
+    want = O.sqr(b) if s is None else O.scale(b, s)
+    assert (bits(gpu_unary(a, b, s)) == bits(want)).all()
+
+
+def test_sqr_and_scale_strided_views_bitwise(hip):
+    rng = np.random.default_rng(32)
+    A = rng.standard_normal((4, 6, 300, 9)).astype(np.float32)
+    for view in (A.transpose(0, 1, 3, 2), A.transpose(3, 2, 1, 0), A[:, ::2, 1:, :]):
+        announce(f"sqr/scale view {view.shape} {view.strides}")
+        assert (bits(gpu_unary(A, view)) == bits(O.sqr(view))).all()
+        assert (bits(gpu_unary(A, view, 2.0)) == bits(O.scale(view, 2.0))).all()
+
+
+def test_sqr_and_scale_reject_bad_shapes(hip):
+    da, out = Dev(np.zeros((4, 8), np.float32)), empty((8, 5))
+    with pytest.raises(H.HipError):
+        H.sqr_f32(da.tensor(), out.tensor())
+    with pytest.raises(H.HipError):
+        H.scale_f32(da.tensor(), out.tensor(), 2.0)
+    da.free()
+    out.free()

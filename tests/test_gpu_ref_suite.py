@@ -26,3 +26,10 @@ def test_reference_golden_programs_on_the_hip_device(hip):
     assert "2 cases run, 0 failed" in r.stdout
     ran = [l for l in r.stdout.splitlines() if "[ OK ]" in l]
     assert len(ran) >= 4, "expected the supported golden cases (add, mul, mul_mat, ...) to run"
+    ok = {l.split("[ OK ]", 1)[1].split()[0] for l in ran if l.split("[ OK ]", 1)[1].split()}
+    # the mul_mat gradient goldens (sum(sqr(mul_mat)) and its backward through
+    # scale, mul, repeat_back, acc and the transposed products) and the unary
+    # goldens of the two ops that path needs
+    for case in ("mul_mat", "mul_mat_batch", "mul_mat_batch_bcast_div", "grad_mul_mat_batch",
+                 "grad_mul_mat_batch_div", "unary_sqr", "scale"):
+        assert case in ok, f"golden case {case} did not run on the HIP device"

@@ -228,6 +228,19 @@ def test_repeat_matches_numpy_tile():
     assert (_bits(O.repeat(a, [3, 8])) == _bits(np.tile(a, (2, 1)))).all()
 
 
+def test_sqr_and_scale_goldens():
+    """The reference suite's PyTorch goldens unary_sqr and scale (s = 2.5), read
+    by its tests/test_golden.cpp (cases tests/golden/reference_suite/cases.txt:9,25)
+    at that program's tolerance (tests/test_golden.cpp:190-201)."""
+    suite = GOLDEN / "reference_suite"
+    a = np.load(suite / "unary_sqr_in0.npy", allow_pickle=False).astype(np.float32)
+    want = np.load(suite / "unary_sqr_out.npy", allow_pickle=False)
+    assert np.allclose(O.sqr(a), want.reshape(a.shape), atol=1e-4, rtol=1e-3)
+    a = np.load(suite / "scale_in0.npy", allow_pickle=False).astype(np.float32)
+    want = np.load(suite / "scale_out.npy", allow_pickle=False)
+    assert np.allclose(O.scale(a, 2.5), want.reshape(a.shape), atol=1e-4, rtol=1e-3)
+
+
 def test_sum_golden():
     a = np.load(GOLDEN / "sum_in0.npy", allow_pickle=False).astype(np.float32)
     want = np.load(GOLDEN / "sum_out.npy", allow_pickle=False).reshape(())
@@ -308,3 +321,49 @@ def test_repeat_bitwise_vs_reference(ashape, pa, d_ne):
     want = O.ref_repeat(A, pa, d_ne)
     av = np.transpose(A, [3 - pa[3 - k] for k in range(4)])
     assert (_bits(O.repeat(av, d_ne)) == _bits(want)).all()
+
+
+# ---------------------------------------------------------------- sqr / scale
+
+def _specials():
+    """Finite values over the exponent range, signed zeros, subnormals, infinities,
+    NaN, and values whose square or scaled value overflows or underflows."""
+    rng = np.random.default_rng(21)
+    v = (rng.standard_normal(4000) * 10.0 ** rng.integers(-40, 39, 4000)).astype(np.float32)
+    extra = np.array([0.0, -0.0, 1e-45, -1e-45, 1e-38, 3.4e38, -3.4e38, 1.8e19, 1.9e19, np.inf, -np.inf, np.nan,
+                      1.0, -1.0, 0.5, 3.0], dtype=np.float32)
+    return np.concatenate([v, extra]).reshape(1, 1, 4, 1004)
+
+
+def test_sqr_is_float32_square():
+    a = _specials()
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = a * a
+    assert (_bits(O.sqr(a)) == _bits(want)).all()
+
+
+@pytest.mark.parametrize("s", [2.0, -0.5, 3.0e-39, 1.0e30, 0.0])
+def test_scale_is_float32_product(s):
+    a = _specials()
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = a * np.float32(s)
+    assert (_bits(O.scale(a, s)) == _bits(want)).all()
+
+
+def test_sqr_and_scale_on_strided_views():
+    rng = np.random.default_rng(22)
+    base = rng.standard_normal((3, 4, 7, 9)).astype(np.float32)
+    v = np.transpose(base, (1, 0, 3, 2))  # every stride non-contiguous
+    assert (_bits(O.sqr(v)) == _bits(np.ascontiguousarray(v * v))).all()
+    assert (_bits(O.scale(v, 1.5)) == _bits(np.ascontiguousarray(v * np.float32(1.5)))).all()
+
+
+@pytestmark_ref
+@pytest.mark.parametrize("pa", [(0, 1, 2, 3), (1, 0, 2, 3), (2, 3, 0, 1)])
+def test_sqr_and_scale_bitwise_vs_reference(pa):
+    rng = np.random.default_rng(23)
+    A = (rng.standard_normal((3, 4, 5, 6)) * 1e3).astype(np.float32)
+    av = np.transpose(A, [3 - pa[3 - k] for k in range(4)])
+    assert (_bits(O.sqr(av)) == _bits(O.ref_unary(A, pa, True))).all()
+    assert (_bits(O.scale(av, 2.0)) == _bits(O.ref_unary(A, pa, False, 2.0))).all()
+    assert (_bits(O.scale(av, -0.37)) == _bits(O.ref_unary(A, pa, False, -0.37))).all()

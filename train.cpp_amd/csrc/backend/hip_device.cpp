@@ -230,6 +230,13 @@ public:
                 if (!tensor_is_contiguous(a) || !tensor_is_contiguous(t)) return false;
                 return acc_region_ok(a, b, acc_params(t));
             }
+            case OP_SQR:    // compute_unary(fn_sqr): one float multiply per element
+            case OP_SCALE: {  // compute_scale: a * s, s in op_params
+                if (!is_f32(a) || !is_f32(t)) return false;
+                for (int k = 0; k < MAX_DIMS; ++k)
+                    if (a->ne[k] != t->ne[k]) return false;
+                return true;
+            }
             case OP_REPEAT_BACK: {
                 if (!is_f32(a) || !is_f32(t) || !tensor_is_contiguous(t)) return false;
                 for (int i = 0; i < 4; ++i) {
@@ -464,6 +471,20 @@ private:
                 const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
                 const trc_hip_tensor d = describe(t, need_buffer(t));
                 check(trc_hip_repeat_back_f32(&a, &d, nullptr), "repeat_back");
+                return;
+            }
+            case OP_SQR: {
+                const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
+                const trc_hip_tensor d = describe(t, need_buffer(t));
+                check(trc_hip_sqr_f32(&a, &d, nullptr), "sqr");
+                return;
+            }
+            case OP_SCALE: {
+                float sc = 0.f;
+                std::memcpy(&sc, t->op_params, sizeof(float));
+                const trc_hip_tensor a = describe(t->src[0], need_buffer(t->src[0]));
+                const trc_hip_tensor d = describe(t, need_buffer(t));
+                check(trc_hip_scale_f32(&a, &d, sc, nullptr), "scale");
                 return;
             }
             default:

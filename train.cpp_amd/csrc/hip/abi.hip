@@ -370,6 +370,20 @@ int trc_hip_repeat_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void*
     return launch_repeat_f32(*a, *dst, (hipStream_t) stream);
 }
 
+int trc_hip_sqr_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream) {
+    TRC_FORCED("trc_hip_sqr_f32");
+    if (a == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_sqr_f32: NULL tensor");
+    if (a->data == nullptr || dst->data == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_sqr_f32: NULL data");
+    return launch_sqr_f32(*a, *dst, (hipStream_t) stream);
+}
+
+int trc_hip_scale_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, float s, void* stream) {
+    TRC_FORCED("trc_hip_scale_f32");
+    if (a == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_scale_f32: NULL tensor");
+    if (a->data == nullptr || dst->data == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_scale_f32: NULL data");
+    return launch_scale_f32(*a, *dst, s, (hipStream_t) stream);
+}
+
 int trc_hip_sum_f32(const trc_hip_tensor* a, const trc_hip_tensor* dst, void* stream) {
     TRC_FORCED("trc_hip_sum_f32");
     if (a == nullptr || dst == nullptr) return fail(TRC_HIP_E_INVALID, "trc_hip_sum_f32: NULL tensor");

@@ -72,6 +72,8 @@ int qm_release_stream(hipStream_t stream);
 int launch_add_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t stream);
 int launch_mul_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t stream);
 int launch_repeat_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t stream);
+int launch_sqr_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t stream);
+int launch_scale_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, float scale, hipStream_t stream);
 int launch_sum_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t stream);
 int launch_acc_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, size_t nb1, size_t nb2,
                    size_t nb3, size_t offset, int inplace, hipStream_t stream);

@@ -86,6 +86,45 @@ __global__ __launch_bounds__(EW_THREADS) void k_binary4(const uint8_t* __restric
     }
 }
 
+enum class UnOp { SQR, SCALE };
+
+// dst[i] = a[i] * a[i] (SQR: fn_sqr, src/backends/cpu/trc_cpu_ops.cpp:86, through
+// compute_unary :119-135) or a[i] * s (SCALE: compute_scale :140-150), element i
+// of dst from element i of a (same shape, any strides): one float multiply each,
+// rows of dst distributed over the grid as in k_binary
+template <UnOp OP>
+__global__ __launch_bounds__(EW_THREADS) void k_unary(const uint8_t* __restrict__ a, Shape4 sa,
+                                                      uint8_t* __restrict__ d, Shape4 sd, float s) {
+    const int64_t rows = sd.ne[1] * sd.ne[2] * sd.ne[3];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const int64_t i1 = r % sd.ne[1], i2 = (r / sd.ne[1]) % sd.ne[2], i3 = r / (sd.ne[1] * sd.ne[2]);
+        const uint8_t* pa = a + i1 * sa.nb[1] + i2 * sa.nb[2] + i3 * sa.nb[3];
+        uint8_t* pd = d + i1 * sd.nb[1] + i2 * sd.nb[2] + i3 * sd.nb[3];
+        for (int64_t i0 = threadIdx.x; i0 < sd.ne[0]; i0 += EW_THREADS) {
+            const float v = *(const float*) (pa + i0 * sa.nb[0]);
+            *(float*) (pd + i0 * sd.nb[0]) = OP == UnOp::SQR ? v * v : v * s;
+        }
+    }
+}
+
+// k_unary with four floats per lane (rows of a and d 16-byte aligned, nb0 == 4,
+// ne0 % 4 == 0); the same single rounding per element
+template <UnOp OP>
+__global__ __launch_bounds__(EW_THREADS) void k_unary4(const uint8_t* __restrict__ a, Shape4 sa,
+                                                       uint8_t* __restrict__ d, Shape4 sd, float s) {
+    const int64_t rows = sd.ne[1] * sd.ne[2] * sd.ne[3];
+    const int64_t n4 = sd.ne[0] / 4;
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const int64_t i1 = r % sd.ne[1], i2 = (r / sd.ne[1]) % sd.ne[2], i3 = r / (sd.ne[1] * sd.ne[2]);
+        const f4* pa = (const f4*) (a + i1 * sa.nb[1] + i2 * sa.nb[2] + i3 * sa.nb[3]);
+        f4* pd = (f4*) (d + i1 * sd.nb[1] + i2 * sd.nb[2] + i3 * sd.nb[3]);
+        for (int64_t q = threadIdx.x; q < n4; q += EW_THREADS) {
+            const f4 v = pa[q];
+            pd[q] = OP == UnOp::SQR ? v * v : v * s;
+        }
+    }
+}
+
 // k_repeat for a dst whose rows are 16-byte aligned with nb0 == 4 and ne0 % 4 ==
 // 0: one row of dst per workgroup pass, four floats per lane and store.
 __global__ __launch_bounds__(EW_THREADS) void k_repeat4(const uint8_t* __restrict__ a, Shape4 sa,
@@ -593,6 +632,37 @@ int launch_add_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_h
 
 int launch_mul_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t s) {
     return launch_binary<BinOp::MUL>("mul", a, b, d, s);
+}
+
+namespace {
+
+template <UnOp OP>
+int launch_unary(const char* name, const trc_hip_tensor& a, const trc_hip_tensor& d, float scale, hipStream_t s) {
+    if (a.type != TRC_HIP_TYPE_F32 || d.type != TRC_HIP_TYPE_F32) return fail(TRC_HIP_E_INVALID, "%s: F32 tensors only", name);
+    if (!shape_ok(a) || !shape_ok(d)) return fail(TRC_HIP_E_SHAPE, "%s: empty or negative extent", name);
+    for (int k = 0; k < 4; ++k) {
+        if (d.ne[k] != a.ne[k]) return fail(TRC_HIP_E_SHAPE, "%s: dst must have a's shape (dim %d)", name, k);
+    }
+    if (!f32_aligned(a) || !f32_aligned(d)) return fail(TRC_HIP_E_ALIGN, "%s: 4-byte alignment", name);
+    const int64_t rows = d.ne[1] * d.ne[2] * d.ne[3];
+    if (rows_vec4(a) && rows_vec4(d)) {
+        hipLaunchKernelGGL(k_unary4<OP>, dim3(grid_for(rows, 1)), dim3(EW_THREADS), 0, s, (const uint8_t*) a.data,
+                           shape_of(a), (uint8_t*) d.data, shape_of(d), scale);
+        return check_launch(name);
+    }
+    hipLaunchKernelGGL(k_unary<OP>, dim3(grid_for(rows, 1)), dim3(EW_THREADS), 0, s, (const uint8_t*) a.data,
+                       shape_of(a), (uint8_t*) d.data, shape_of(d), scale);
+    return check_launch(name);
+}
+
+}  // namespace
+
+int launch_sqr_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t s) {
+    return launch_unary<UnOp::SQR>("sqr", a, d, 0.f, s);
+}
+
+int launch_scale_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, float scale, hipStream_t s) {
+    return launch_unary<UnOp::SCALE>("scale", a, d, scale, s);
 }
 
 int launch_repeat_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t s) {

@@ -25,7 +25,7 @@ EXPORTS = (
     "trc_hip_fill_f32", "trc_hip_dequant", "trc_hip_mul_mat_f32", "trc_hip_qmatvec", "trc_hip_cpy",
     "trc_hip_add_f32", "trc_hip_acc_f32", "trc_hip_repeat_back_f32", "trc_hip_qmatvec_noalloc",
     "trc_hip_mul_f32", "trc_hip_repeat_f32", "trc_hip_sum_f32", "trc_hip_qmatvec_release_stream",
-    "trc_hip_mul_mat_acc_f32",
+    "trc_hip_mul_mat_acc_f32", "trc_hip_sqr_f32", "trc_hip_scale_f32",
 )
 
 
@@ -94,6 +94,8 @@ def load() -> C.CDLL:
         "trc_hip_dequant": ([I, P, I64, P, P], I),
         "trc_hip_mul_mat_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
         "trc_hip_mul_mat_acc_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), P], I),
+        "trc_hip_sqr_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), P], I),
+        "trc_hip_scale_f32": ([C.POINTER(Tensor), C.POINTER(Tensor), C.c_float, P], I),
         "trc_hip_qmatvec": ([I, P, I64, I64, SZ, P, I64, SZ, P, SZ, P], I),
         "trc_hip_qmatvec_noalloc": ([I, P, I64, I64, SZ, P, I64, SZ, P, SZ, P], I),
         "trc_hip_qmatvec_release_stream": ([P], I),
@@ -146,6 +148,16 @@ def dequant(type_: int, blocks_ptr: int, n_blocks: int, dst_ptr: int, stream: in
 
 def mul_mat_f32(a: Tensor, b: Tensor, d: Tensor, stream: int | None = None) -> None:
     check(load().trc_hip_mul_mat_f32(C.byref(a), C.byref(b), C.byref(d), stream))
+
+
+def sqr_f32(a: Tensor, d: Tensor, stream: int | None = None) -> None:
+    """d = a * a (trc_hip_sqr_f32)."""
+    check(load().trc_hip_sqr_f32(C.byref(a), C.byref(d), stream))
+
+
+def scale_f32(a: Tensor, d: Tensor, s: float, stream: int | None = None) -> None:
+    """d = a * s (trc_hip_scale_f32)."""
+    check(load().trc_hip_scale_f32(C.byref(a), C.byref(d), s, stream))
 
 
 def mul_mat_acc_f32(a: Tensor, b: Tensor, d: Tensor, stream: int | None = None) -> None:
