@@ -71,7 +71,10 @@ constexpr uint32_t MM_OUT = 0x80000000u;         // an offset past the resource:
 // pitch of ROWS + 4, 20 % of the forward product's LDS cycles were
 // bank-conflict stalls, and 4-way conflicts made 128 x 64 tiles at BK = 32 11 %
 // slower.) The other loaders store float4s, whose rows stay 16-byte aligned.
-template <int MODE, int ROWS, int BK, int THREADS>
+// KI (k-contiguous only): the slab is stored as planes of k pairs, element
+// (k, row) at (k / 2) * 2 * LD + 2 * row + k % 2, so one 8-byte read gives a
+// lane the two k of a row that two consecutive MFMAs take from it.
+template <int MODE, int ROWS, int BK, int THREADS, bool KI = false>
 struct SlabLoader {
     static_assert(MODE != K_CONTIG || BK % 16 == 0, "k-contiguous slabs come in 16-k groups");
     static constexpr int LD = MODE == K_CONTIG ? ROWS + 2 : ROWS + 4;
@@ -133,8 +136,13 @@ struct SlabLoader {
                 const int q = tid + THREADS * u;
                 const int row = (q >> 2) % ROWS;
                 const int kq = (q & 3) + 4 * (q / (4 * ROWS));
+                if constexpr (KI) {
+                    *(float2*) (lds + (2 * kq) * 2 * LD + 2 * row) = float2{r[4 * u + 0], r[4 * u + 1]};
+                    *(float2*) (lds + (2 * kq + 1) * 2 * LD + 2 * row) = float2{r[4 * u + 2], r[4 * u + 3]};
+                } else {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) lds[(4 * kq + c) * LD + row] = r[4 * u + c];
+                    for (int c = 0; c < 4; ++c) lds[(4 * kq + c) * LD + row] = r[4 * u + c];
+                }
             }
         } else if constexpr (MODE == R_CONTIG) {
 #pragma unroll
@@ -157,15 +165,15 @@ struct SlabLoader {
 
 // SPLIT: parts of K (1, or 2 summed into a cleared dst with atomic adds).
 // ACC: dst += the product (K in one part).
-template <int WI, int WJ, int TI, int TJ, int BK, int AMODE, int BMODE, int SPLIT, bool ACC = false>
+template <int WI, int WJ, int TI, int TJ, int BK, int AMODE, int BMODE, int SPLIT, bool ACC = false, bool KI = false>
 __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
     constexpr int THREADS = WI * WJ * 64;
     static_assert(SPLIT == 1 || SPLIT == 2, "two parts at most keep the atomic sums deterministic");
     static_assert(!ACC || SPLIT == 1, "d + a + b would round differently from d + (a + b)");
     constexpr int BM = WI * TI * 32;  // tile extent along i
     constexpr int BN = WJ * TJ * 32;  // tile extent along j
-    using LA = SlabLoader<AMODE, BM, BK, THREADS>;
-    using LB = SlabLoader<BMODE, BN, BK, THREADS>;
+    using LA = SlabLoader<AMODE, BM, BK, THREADS, KI && AMODE == K_CONTIG>;
+    using LB = SlabLoader<BMODE, BN, BK, THREADS, KI && BMODE == K_CONTIG>;
     __shared__ __attribute__((aligned(16))) float As[BK * LA::LD];
     __shared__ __attribute__((aligned(16))) float Bs[BK * LB::LD];
 
@@ -230,19 +238,54 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
         // (dW 142 -> 136 us, configuration 4 168 -> 161 us, same bits). The split
         // products run one workgroup per CU, where it measured no gain.
         if constexpr (SPLIT == 1) __builtin_amdgcn_s_setprio(1);
+        if constexpr (KI) {
+            // k in groups of 4: the first MFMA of a group takes k = 4t + 2 half, the
+            // second 4t + 2 half + 1, from both operands
 #pragma unroll
-        for (int s = 0; s < BK / 2; ++s) {
-            const int kr = 2 * s + half;
-            float av[TI], bv[TJ];
+            for (int t4 = 0; t4 < BK / 4; ++t4) {
+                const int k0 = 4 * t4 + 2 * half;
+                float2 av[TI], bv[TJ];
 #pragma unroll
-            for (int x = 0; x < TI; ++x) av[x] = As[kr * LA::LD + (wi * TI + x) * 32 + col];
+                for (int x = 0; x < TI; ++x) {
+                    const int r = (wi * TI + x) * 32 + col;
+                    if constexpr (AMODE == K_CONTIG) {
+                        av[x] = *(const float2*) (As + (k0 >> 1) * 2 * LA::LD + 2 * r);
+                    } else {
+                        av[x] = float2{As[k0 * LA::LD + r], As[(k0 + 1) * LA::LD + r]};
+                    }
+                }
 #pragma unroll
-            for (int y = 0; y < TJ; ++y) bv[y] = Bs[kr * LB::LD + (wj * TJ + y) * 32 + col];
+                for (int y = 0; y < TJ; ++y) {
+                    const int r = (wj * TJ + y) * 32 + col;
+                    if constexpr (BMODE == K_CONTIG) {
+                        bv[y] = *(const float2*) (Bs + (k0 >> 1) * 2 * LB::LD + 2 * r);
+                    } else {
+                        bv[y] = float2{Bs[k0 * LB::LD + r], Bs[(k0 + 1) * LB::LD + r]};
+                    }
+                }
 #pragma unroll
-            for (int x = 0; x < TI; ++x)
+                for (int x = 0; x < TI; ++x)
 #pragma unroll
-                for (int y = 0; y < TJ; ++y)
-                    acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[y], av[x], acc[x][y], 0, 0, 0);
+                    for (int y = 0; y < TJ; ++y) {
+                        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[y].x, av[x].x, acc[x][y], 0, 0, 0);
+                        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[y].y, av[x].y, acc[x][y], 0, 0, 0);
+                    }
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < BK / 2; ++s) {
+                const int kr = 2 * s + half;
+                float av[TI], bv[TJ];
+#pragma unroll
+                for (int x = 0; x < TI; ++x) av[x] = As[kr * LA::LD + (wi * TI + x) * 32 + col];
+#pragma unroll
+                for (int y = 0; y < TJ; ++y) bv[y] = Bs[kr * LB::LD + (wj * TJ + y) * 32 + col];
+#pragma unroll
+                for (int x = 0; x < TI; ++x)
+#pragma unroll
+                    for (int y = 0; y < TJ; ++y)
+                        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[y], av[x], acc[x][y], 0, 0, 0);
+            }
         }
         if constexpr (SPLIT == 1) __builtin_amdgcn_s_setprio(0);
         if (more) {
@@ -571,7 +614,7 @@ int pick_mode(const trc_hip_tensor& t, int64_t rows) {
     return GENERIC;
 }
 
-template <int WI, int WJ, int TI, int TJ, int BK, int AM, int BMO, int SPLIT, bool ACC>
+template <int WI, int WJ, int TI, int TJ, int BK, int AM, int BMO, int SPLIT, bool ACC, bool KI = false>
 int launch_cfg(MMArgs& p, int64_t planes, hipStream_t stream) {
     constexpr int BM = WI * TI * 32, BN = WJ * TJ * 32;
     p.tiles_i = (p.M + BM - 1) / BM;
@@ -580,7 +623,7 @@ int launch_cfg(MMArgs& p, int64_t planes, hipStream_t stream) {
     if (grid > 0x7FFFFFFF) return fail(TRC_HIP_E_SHAPE, "mul_mat: %lld workgroups exceed one launch", (long long) grid);
     p.xcd_planes = planes % 8 == 0 ? 1 : 0;
     p.d_span = (p.M - 1) * p.d_nb0 + (p.N - 1) * p.d_nb1 + 4;
-    hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, BK, AM, BMO, SPLIT, ACC>), dim3((unsigned) grid),
+    hipLaunchKernelGGL((k_mul_mat<WI, WJ, TI, TJ, BK, AM, BMO, SPLIT, ACC, KI>), dim3((unsigned) grid),
                        dim3(WI * WJ * 64), 0, stream, p);
     return check_launch("mul_mat_f32");
 }
@@ -661,6 +704,12 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
     if (dense_dst && p.K >= 1024 && 2 * big_tiles >= device_cus()) {
         const int rc = launch_fill_f32((float*) d.data, 0.f, p.M * p.N * planes, stream);
         if (rc != TRC_HIP_OK) return rc;
+        // a transposed src0 against a k-contiguous src1 (the dX product of a
+        // Linear layer): k-paired LDS planes for src1, 4 % faster there; 1.5 %
+        // slower with both operands k-contiguous (the forward product)
+        if (am == R_CONTIG && bm == K_CONTIG) {
+            return launch_cfg<2, 4, 2, 1, 32, R_CONTIG, K_CONTIG, 2, false, true>(p, planes, stream);
+        }
         return dispatch_modes<2, 4, 2, 1, 32, 2>(p, am, bm, planes, stream);
     }
     return dispatch_modes<2, 2, 1, 1, 32, 1>(p, am, bm, planes, stream);
