@@ -143,7 +143,14 @@ int trc_hip_dequant(int type, const void* blocks, int64_t n_blocks, float* dst, 
  * All three tensors are TRC_HIP_TYPE_F32 with 4-byte aligned data and strides.
  * The sum is reordered, so results match the CPU to rounding, not bit for bit;
  * they are the same from run to run. dst must not overlap a or b: for some
- * shapes it is cleared first and the halves of the sum over k are added into it. */
+ * shapes (K >= 1024, between half and two 128 x 128 output tiles per CU, a
+ * contiguous dst) the two halves of the sum over k meet in dst, one stored and
+ * the other added, ordered through 32 KiB of ticket words kept past the end of
+ * the stream's workspace of trc_hip_qmatvec. The first such call on a stream
+ * allocates that workspace (make it before capturing the stream into a graph
+ * in global capture mode); the rules for that workspace below hold here too:
+ * calls on different streams may overlap, a captured graph keeps the words of
+ * the stream it was captured on, and trc_hip_qmatvec_release_stream frees them. */
 int trc_hip_mul_mat_f32(const trc_hip_tensor* a, const trc_hip_tensor* b,
                         const trc_hip_tensor* dst, void* stream);
 
@@ -193,7 +200,8 @@ int trc_hip_qmatvec(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w
 /* Frees the x workspace trc_hip_qmatvec keeps for `stream` on the current
  * device, after waiting for the stream's queued work (hipStreamSynchronize).
  * Call it before hipStreamDestroy; a later call on the stream allocates a new
- * workspace. trc_hip_sum_f32 keeps its row sums in the same workspace.
+ * workspace. trc_hip_sum_f32 keeps its row sums in the same workspace, and
+ * trc_hip_mul_mat_f32 its ticket words past its end.
  * hipStreamPerThread is keyed by the calling thread. Returns TRC_HIP_OK when
  * the stream has no workspace. No counterpart in the reference:
  * it bounds the memory of trc_hip_qmatvec's per-stream workspaces, like the

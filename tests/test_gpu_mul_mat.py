@@ -10,7 +10,7 @@ import pytest
 
 import oracle_lib as O
 from conftest import GOLDEN, announce
-from gpu_util import Dev, empty, gpu_mul_mat
+from gpu_util import Dev, Stream, empty, gpu_mul_mat
 from traincpp_amd import hip as H
 from traincpp_amd import synth
 
@@ -106,8 +106,8 @@ def test_backward_goldens(hip, case):
     # K, M, N, b2, b3, a2, a3
     (1, 1, 1, 1, 1, 1, 1), (2, 33, 31, 1, 1, 1, 1), (17, 65, 129, 1, 1, 1, 1), (100, 130, 70, 3, 2, 3, 1),
     (256, 256, 256, 1, 1, 1, 1), (513, 200, 300, 2, 1, 1, 1), (64, 128, 128, 4, 2, 2, 2), (7, 9, 11, 6, 1, 3, 1),
-    # 128 or more 128x128 tiles but under 512 and K >= 1024: K in two parts summed
-    # by atomic adds (partial tiles, K not a multiple of the slab, two planes)
+    # 128 or more 128x128 tiles but under 512 and K >= 1024: K in two parts that
+    # meet in dst (partial tiles, K not a multiple of the slab, two planes)
     (2500, 2000, 1000, 1, 1, 1, 1), (1030, 1000, 1000, 1, 1, 2, 1),
     # plane counts that are a multiple of 8 (each plane's tiles on one XCD):
     # ragged 64x64 tiles over 8 planes, ragged 128x128 tiles over 64 planes
@@ -224,6 +224,38 @@ def test_config4_broadcast_permuted(hip):
     assert sums_error(got, da.base, bv) <= 1e-5
     da.free()
     db.free()
+
+
+def test_split_products_on_two_streams(hip):
+    """K split in two (K >= 1024, 128 to 511 tiles of 128 x 128): the waves holding
+    one block in the two parts meet in dst through ticket words kept with the
+    stream's workspace, which every launch leaves clear. Two such products
+    alternate on two streams, 20 calls each, so that they overlap on the GPU and
+    each stream needs its own words. Each result equals, bit for bit, the same
+    product run twice more on the null stream, and matches the oracle."""
+    K, M, N = 1024, 2048, 1024  # 16 x 8 tiles
+    streams = [Stream(), Stream()]
+    cases = []
+    for c in range(2):
+        A = synth.normal(940 + c, K * M).reshape(1, 1, M, K)
+        B = synth.normal(950 + c, K * N).reshape(1, 1, N, K) * np.float32(10.0 ** c)
+        cases.append((A, B, Dev(A), Dev(B), empty((1, 1, N, M))))
+    announce("mul_mat K split, two streams")
+    for _ in range(20):
+        for c, (A, B, da, db, dd) in enumerate(cases):
+            H.mul_mat_f32(da.tensor(), db.tensor(), dd.tensor(), streams[c].handle)
+    for st in streams:
+        H.sync(st.handle)
+    for A, B, da, db, dd in cases:
+        got = dd.read()
+        for _ in range(2):
+            alone = gpu_mul_mat(da, da.base, db, db.base)
+            assert np.array_equal(got.view(np.uint32), alone.view(np.uint32))
+        assert O.row_l2_error(got, O.mul_mat(A, B, threads=8)) <= TOL
+        for dv in (da, db, dd):
+            dv.free()
+    for st in streams:
+        st.close()
 
 
 def test_shape_errors_are_rejected(hip):
@@ -377,8 +409,8 @@ def test_mul_mat_acc_adds_the_product(hip, shape):
 
 
 def test_mul_mat_acc_keeps_k_whole(hip):
-    """Configuration 3's forward shape, whose plain product sums K in two parts into
-    a cleared dst: added into dst it keeps K whole (d + a + b would round differently
+    """Configuration 3's forward shape, whose plain product sums K in two parts that
+    meet in dst: added into dst it keeps K whole (d + a + b would round differently
     from d + (a + b)), and is checked against d0 + the oracle's product."""
     announce("mul_mat_acc configuration 3 forward shape")
     K, M, N = 4096, 4096, 512

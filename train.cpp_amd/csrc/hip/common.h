@@ -69,6 +69,11 @@ int qm_static_scratch(uint8_t** ws);
 int qm_stream_workspace(hipStream_t stream, uint8_t** ws);
 // Waits for `stream` and frees its workspace on the current device (if any).
 int qm_release_stream(hipStream_t stream);
+// The ticket words of the K-split mul_mat (two per wave of every tile, at most
+// MM_TICKETS of them), kept past the end of the stream's workspace: zero when
+// the workspace is made, and left zero by every launch that uses them.
+constexpr int MM_TICKETS = 512 * 8 * 2;
+int mm_stream_tickets(hipStream_t stream, uint32_t** tickets);
 int launch_add_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t stream);
 int launch_mul_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d, hipStream_t stream);
 int launch_repeat_f32(const trc_hip_tensor& a, const trc_hip_tensor& d, hipStream_t stream);

@@ -32,9 +32,11 @@
 //     each src0 plane) is read into one L2 only; otherwise tiles follow the
 //     grid order, where the tiles sharing one src0 row block meet on one XCD.
 //   - When 128x128 tiles would give under two workgroups per CU, K is split in
-//     two: 8-wave workgroups (64x32 per wave) each sum half of K for one tile,
-//     into a dst cleared beforehand, with float atomic adds. 0 + a + b rounds
-//     the same in either order, so results stay deterministic.
+//     two: 8-wave workgroups (64x32 per wave) each sum half of K for one tile.
+//     The two waves that hold one 64x32 block meet in dst without a clear: each
+//     takes a ticket; the first stores its sums, the second adds its own with
+//     float atomics once the first's are in. a + b is the same in either order,
+//     so results stay deterministic.
 //   - Up to 64 columns against a k-contiguous src0 (decode-sized batches) take
 //     k_mm_skinny below instead: one pass over src0 on every CU.
 #include "common.h"
@@ -56,10 +58,12 @@ struct MMArgs {
     int64_t tiles_i, tiles_j;
     int xcd_planes;  // 1: planes % 8 == 0, tiles of plane p on XCD p % 8
     int64_t d_span;  // bytes from a dst plane's first element to past its last
+    uint32_t* tickets;  // K split in two: two words per wave of every tile, zero between launches
 };
 
 constexpr uint32_t MM_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
 constexpr uint32_t MM_OUT = 0x80000000u;         // an offset past the resource: loads read 0, stores drop
+constexpr int MM_FLAG_POLLS = 1 << 20;           // cap on the K-split combine's wait (seconds of polling)
 
 // Loads a ROWS x BK slab (rows = i for src0, j for src1) of one operand into
 // registers, then stores it to LDS as lds[k * LD + row]. The k-contiguous
@@ -163,7 +167,7 @@ struct SlabLoader {
     }
 };
 
-// SPLIT: parts of K (1, or 2 summed into a cleared dst with atomic adds).
+// SPLIT: parts of K (1, or 2 meeting in dst through the stream's ticket words).
 // ACC: dst += the product (K in one part).
 template <int WI, int WJ, int TI, int TJ, int BK, int AMODE, int BMODE, int SPLIT, bool ACC = false, bool KI = false>
 __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
@@ -191,6 +195,7 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
     }
     const int part = SPLIT > 1 ? (int) (t % SPLIT) : 0;
     t /= SPLIT;
+    const int64_t tile = t;
     const int64_t ti = t % p.tiles_i;
     t /= p.tiles_i;
     const int64_t tj = t % p.tiles_j;
@@ -353,6 +358,62 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
         }
         return;
     }
+    if constexpr (SPLIT > 1) {
+        // dst element of accumulator register v of tile (x, y), or null past dst
+        auto out = [&](int x, int y, int v) -> float* {
+            const int64_t i = i0 + (wi * TI + x) * 32 + col;
+            const int64_t j = j0 + (wj * TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            return i < p.M && j < p.N ? (float*) (d + i * p.d_nb0 + j * p.d_nb1) : nullptr;
+        };
+        // The waves holding this 64 x 32 block in the two parts meet through two
+        // words: a ticket, then a flag. The first to take the ticket stores its
+        // sums with agent-scope stores (written through to where every XCD reads
+        // them), waits until all of them are done and raises the flag. The
+        // second waits for the flag, adds its sums with float atomics (performed
+        // where the stores landed) and clears both words for the next launch on
+        // the stream. The wait is only for a wave that already holds its ticket
+        // and has nothing left to wait for, so it ends; a cap on the polls (far
+        // above the microseconds it takes) keeps it bounded regardless. Against
+        // a cleared dst with an atomic add from each part, this leaves out the
+        // clearing launch and half of the atomics (configuration 3's forward and
+        // dX products 156.7 -> 150.5 and 155.6 -> 149.4 us), with the same sums.
+        uint32_t* tk = p.tickets + 2 * (tile * (WI * WJ) + wave);
+        uint32_t first = 0;
+        if (lane == 0) first = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(first) == 0) {
+#pragma unroll
+            for (int x = 0; x < TI; ++x)
+#pragma unroll
+                for (int y = 0; y < TJ; ++y)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        if (float* o = out(x, y, v))
+                            __hip_atomic_store(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (lane == 0) __hip_atomic_store(tk + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        if (lane == 0) {
+            for (int n = 0; n < MM_FLAG_POLLS; ++n) {
+                if (__hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int x = 0; x < TI; ++x)
+#pragma unroll
+            for (int y = 0; y < TJ; ++y)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    if (float* o = out(x, y, v))
+                        __hip_atomic_fetch_add(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+            __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(tk + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
 #pragma unroll
     for (int x = 0; x < TI; ++x) {
         const int64_t i = i0 + (wi * TI + x) * 32 + col;
@@ -363,14 +424,9 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
             for (int v = 0; v < 16; ++v) {
                 const int64_t j = j0 + (wj * TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
                 if (j >= p.N) continue;
-                float* dst = (float*) (d + i * p.d_nb0 + j * p.d_nb1);
-                if constexpr (SPLIT > 1) {
-                    __hip_atomic_fetch_add(dst, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                } else {
-                    // Non-temporal: dst is not read again by this launch (dW
-                    // 1 % and configuration 4 2 % faster than plain stores).
-                    __builtin_nontemporal_store(acc[x][y][v], dst);
-                }
+                // Non-temporal: dst is not read again by this launch (dW 1 % and
+                // configuration 4 2 % faster than plain stores).
+                __builtin_nontemporal_store(acc[x][y][v], (float*) (d + i * p.d_nb0 + j * p.d_nb1));
             }
         }
     }
@@ -650,6 +706,7 @@ int dispatch_modes(MMArgs& p, int am, int bm, int64_t planes, hipStream_t s) {
 int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const trc_hip_tensor& d,
                        hipStream_t stream, bool accumulate) {
     MMArgs p;
+    p.tickets = nullptr;
     p.a = (const uint8_t*) a.data;
     p.b = (const uint8_t*) b.data;
     p.d = (uint8_t*) d.data;
@@ -691,7 +748,8 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
 
     // Large tiles when they still give every CU at least two workgroups. With
     // between half and two tiles per CU and a long K, large tiles with K in two
-    // parts (into a cleared, contiguous dst); otherwise 64x64 tiles.
+    // parts (into a contiguous dst; the parts meet through ticket words in the
+    // stream's workspace); otherwise 64x64 tiles.
     const int64_t big_tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128) * planes;
     if (accumulate) {
         // K stays in one part: the large tiles when they fill the CUs twice, else 64 x 64
@@ -702,7 +760,8 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
     const bool dense_dst = p.d_nb0 == 4 && p.d_nb1 == 4 * p.M && p.d_nb2 == p.d_nb1 * p.N &&
                            p.d_nb3 == p.d_nb2 * b.ne[2];
     if (dense_dst && p.K >= 1024 && 2 * big_tiles >= device_cus()) {
-        const int rc = launch_fill_f32((float*) d.data, 0.f, p.M * p.N * planes, stream);
+        static_assert(511 * 8 * 2 <= MM_TICKETS, "two ticket words per wave of under 512 tiles");
+        const int rc = mm_stream_tickets(stream, &p.tickets);
         if (rc != TRC_HIP_OK) return rc;
         // a transposed src0 against a k-contiguous src1 (the dX product of a
         // Linear layer): k-paired LDS planes for src1, 4 % faster there; 1.5 %

@@ -989,6 +989,10 @@ int launch_qmm(int type, const void* wq, int64_t K, int64_t M, size_t nb1_w, con
 // QM_STREAM_WS workspaces are kept per device: a new stream past that waits for
 // the device to go idle and takes over the least recently used one.
 // trc_hip_qmatvec_release_stream frees a stream's workspace after its work.
+// Past its QM_WS_BYTES the workspace holds the ticket words of the K-split
+// mul_mat (MM_TICKETS words, cleared by a fill kernel on the stream when the
+// workspace is made; every launch that takes a ticket leaves it zero again, so
+// a workspace handed to another stream after the device went idle is clear).
 //
 // trc_hip_qmatvec_noalloc: the file-scope device array `scratch` below. Each GPU
 // holds its own copy at its own address, found once per device with
@@ -1101,10 +1105,23 @@ int qm_stream_workspace(hipStream_t s, uint8_t** ws) {
         return TRC_HIP_OK;
     }
     void* p = nullptr;
-    const hipError_t e = hipMalloc(&p, QM_WS_BYTES);
+    const hipError_t e = hipMalloc(&p, QM_WS_BYTES + MM_TICKETS * sizeof(uint32_t));
     if (e != hipSuccess) return hip_error(e, "qmatvec: x workspace for a new stream (hipMalloc)");
+    const int frc = launch_fill_f32((float*) ((uint8_t*) p + QM_WS_BYTES), 0.f, MM_TICKETS, s);
+    if (frc != TRC_HIP_OK) {
+        (void) hipFree(p);
+        return frc;
+    }
     v.push_back({dev, s, tid, (uint8_t*) p, ++g_ws_clock});
     *ws = (uint8_t*) p;
+    return TRC_HIP_OK;
+}
+
+int mm_stream_tickets(hipStream_t s, uint32_t** tickets) {
+    uint8_t* ws = nullptr;
+    const int rc = qm_stream_workspace(s, &ws);
+    if (rc != TRC_HIP_OK) return rc;
+    *tickets = (uint32_t*) (ws + QM_WS_BYTES);
     return TRC_HIP_OK;
 }
 
