@@ -33,6 +33,47 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     return (float) __builtin_bit_cast(_Float16, (uint16_t) h);
 }
 
+// Two parts of a sum split in two meet in dst without a cleared dst. For each
+// block of outputs, the wave holding it in each part takes a ticket from
+// tk[0]. The first stores its sums with agent-scope stores (written through to
+// where every XCD reads them), waits until all of them are done and raises the
+// flag tk[1]. The second waits for the flag, adds its sums with float atomics
+// (performed where the stores landed) and clears both words for the next
+// launch. a + b is the same in either order, so results do not depend on which
+// part comes first. The wait is only for a wave that already holds its ticket
+// and has nothing left to wait for, so it ends; a cap on the polls (seconds,
+// against the microseconds it takes) bounds it regardless.
+constexpr int TICKET_FLAG_POLLS = 1 << 20;
+
+// Whether this wave is the first of the two (lane 0 takes the ticket).
+__device__ __forceinline__ bool ticket_first(uint32_t* tk, int lane) {
+    uint32_t first = 0;
+    if (lane == 0) first = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_amdgcn_readfirstlane(first) == 0;
+}
+// The first, after its agent-scope stores: waits for them, then raises the flag.
+__device__ __forceinline__ void ticket_publish(uint32_t* tk, int lane) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) __hip_atomic_store(tk + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The second, before its atomic adds: waits for the flag.
+__device__ __forceinline__ void ticket_wait(uint32_t* tk, int lane) {
+    if (lane == 0) {
+        for (int n = 0; n < TICKET_FLAG_POLLS; ++n) {
+            if (__hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+// The second, after its adds: both words back to zero.
+__device__ __forceinline__ void ticket_clear(uint32_t* tk, int lane) {
+    if (lane == 0) {
+        __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(tk + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // Launch-side error reporting, implemented in abi.hip.
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);

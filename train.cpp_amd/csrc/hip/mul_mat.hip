@@ -63,7 +63,6 @@ struct MMArgs {
 
 constexpr uint32_t MM_RSRC_WORD3 = 0x00020000u;  // gfx9 buffer resource: raw 32-bit dwords
 constexpr uint32_t MM_OUT = 0x80000000u;         // an offset past the resource: loads read 0, stores drop
-constexpr int MM_FLAG_POLLS = 1 << 20;           // cap on the K-split combine's wait (seconds of polling)
 
 // Loads a ROWS x BK slab (rows = i for src0, j for src1) of one operand into
 // registers, then stores it to LDS as lds[k * LD + row]. The k-contiguous
@@ -366,21 +365,13 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
             return i < p.M && j < p.N ? (float*) (d + i * p.d_nb0 + j * p.d_nb1) : nullptr;
         };
         // The waves holding this 64 x 32 block in the two parts meet through two
-        // words: a ticket, then a flag. The first to take the ticket stores its
-        // sums with agent-scope stores (written through to where every XCD reads
-        // them), waits until all of them are done and raises the flag. The
-        // second waits for the flag, adds its sums with float atomics (performed
-        // where the stores landed) and clears both words for the next launch on
-        // the stream. The wait is only for a wave that already holds its ticket
-        // and has nothing left to wait for, so it ends; a cap on the polls (far
-        // above the microseconds it takes) keeps it bounded regardless. Against
-        // a cleared dst with an atomic add from each part, this leaves out the
-        // clearing launch and half of the atomics (configuration 3's forward and
-        // dX products 156.7 -> 150.5 and 155.6 -> 149.4 us), with the same sums.
+        // ticket words (ticket_first and the protocol it begins, common.h).
+        // Against a cleared dst with an atomic add from each part, this leaves
+        // out the clearing launch and half of the atomics (configuration 3's
+        // forward and dX products 156.7 -> 150.5 and 155.6 -> 149.4 us), with
+        // the same sums.
         uint32_t* tk = p.tickets + 2 * (tile * (WI * WJ) + wave);
-        uint32_t first = 0;
-        if (lane == 0) first = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (__builtin_amdgcn_readfirstlane(first) == 0) {
+        if (ticket_first(tk, lane)) {
 #pragma unroll
             for (int x = 0; x < TI; ++x)
 #pragma unroll
@@ -389,17 +380,10 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
                     for (int v = 0; v < 16; ++v)
                         if (float* o = out(x, y, v))
                             __hip_atomic_store(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            if (lane == 0) __hip_atomic_store(tk + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ticket_publish(tk, lane);
             return;
         }
-        if (lane == 0) {
-            for (int n = 0; n < MM_FLAG_POLLS; ++n) {
-                if (__hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        ticket_wait(tk, lane);
 #pragma unroll
         for (int x = 0; x < TI; ++x)
 #pragma unroll
@@ -408,10 +392,7 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
                 for (int v = 0; v < 16; ++v)
                     if (float* o = out(x, y, v))
                         __hip_atomic_fetch_add(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (lane == 0) {
-            __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(tk + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        ticket_clear(tk, lane);
         return;
     }
 #pragma unroll
