@@ -109,6 +109,9 @@ def test_backward_goldens(hip, case):
     # 128 or more 128x128 tiles but under 512 and K >= 1024: K in two parts that
     # meet in dst (partial tiles, K not a multiple of the slab, two planes)
     (2500, 2000, 1000, 1, 1, 1, 1), (1030, 1000, 1000, 1, 1, 2, 1),
+    # the same with whole tiles and slabs (double-buffered slabs): broadcast
+    # planes, and 8 planes (each plane's tiles on one XCD)
+    (1024, 1024, 512, 4, 1, 2, 1), (1088, 512, 512, 8, 1, 1, 1),
     # plane counts that are a multiple of 8 (each plane's tiles on one XCD):
     # ragged 64x64 tiles over 8 planes, ragged 128x128 tiles over 64 planes
     (33, 70, 90, 4, 2, 1, 1), (40, 300, 300, 8, 8, 1, 1),
@@ -231,12 +234,12 @@ def test_split_products_on_two_streams(hip):
     one block in the two parts meet in dst through ticket words kept with the
     stream's workspace, which every launch leaves clear. Two such products
     alternate on two streams, 20 calls each, so that they overlap on the GPU and
-    each stream needs its own words. Each result equals, bit for bit, the same
+    each stream needs its own words: one with whole tiles (double-buffered
+    slabs), one with ragged tiles. Each result equals, bit for bit, the same
     product run twice more on the null stream, and matches the oracle."""
-    K, M, N = 1024, 2048, 1024  # 16 x 8 tiles
     streams = [Stream(), Stream()]
     cases = []
-    for c in range(2):
+    for c, (K, M, N) in enumerate([(1024, 2048, 1024), (1100, 2000, 1000)]):  # 16 x 8 tiles each
         A = synth.normal(940 + c, K * M).reshape(1, 1, M, K)
         B = synth.normal(950 + c, K * N).reshape(1, 1, N, K) * np.float32(10.0 ** c)
         cases.append((A, B, Dev(A), Dev(B), empty((1, 1, N, M))))

@@ -36,10 +36,14 @@
 //     The two waves that hold one 64x32 block meet in dst without a clear: each
 //     takes a ticket; the first stores its sums, the second adds its own with
 //     float atomics once the first's are in. a + b is the same in either order,
-//     so results stay deterministic.
+//     so results stay deterministic. With whole tiles and float4 loaders the
+//     split products take k_mul_mat_db: two LDS slab buffers, the stores and
+//     loads of the next slabs spread between the MFMAs, one barrier per slab.
 //   - Up to 64 columns against a k-contiguous src0 (decode-sized batches) take
 //     k_mm_skinny below instead: one pass over src0 on every CU.
 #include "common.h"
+
+#include <type_traits>
 
 namespace trc_hip {
 namespace {
@@ -413,6 +417,206 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
     }
 }
 
+// ------------------------------------------------ K split in two, whole tiles
+//
+// The products whose K is split in two (one 8-wave workgroup per CU for a
+// 128 x 128 tile and half of K), when every tile and slab is whole (M and N
+// multiples of 128, K of 64) and both operands load as float4s (k- or
+// row-contiguous). k_mul_mat stores each slab between two barriers while no
+// MFMA runs; here two LDS slab buffers take turns: during the MFMAs of slab s
+// the registers holding slab s + 1 are stored into the other buffer (from
+// k-step DB_S0 on, one float4 per k-step) and then refilled with slab s + 2
+// (from k-step DB_L0 on), with one barrier per slab. Whole tiles need no bounds
+// checks, which keeps the slab loop free of branches and selects (with
+// clamped addresses and selects the same schedule measured 157-160 us, slower
+// than k_mul_mat). Both operands are read as k-paired LDS planes where they
+// are k-contiguous, so the MFMAs take k in groups of 4 (k = 4t + 2 half, then
+// 4t + 2 half + 1). Configuration 3 (interleaved minimums, one box): forward
+// 149.5 -> 139.5 us (its sums now group k by pairs, within 6e-5 of 281), dX
+// 148.8 -> 146.0 us (same bits). The two parts meet in dst through the
+// stream's ticket words as in k_mul_mat.
+constexpr int DB_WI = 2, DB_WJ = 4, DB_TI = 2, DB_TJ = 1, DB_BK = 32, DB_S0 = 2, DB_L0 = 8;
+constexpr int DB_THREADS = DB_WI * DB_WJ * 64;
+constexpr int DB_BM = DB_WI * DB_TI * 32, DB_BN = DB_WJ * DB_TJ * 32;
+
+// One operand's slab as NU float4 pieces per thread: the K_CONTIG mapping of
+// SlabLoader (4 lanes per 64 contiguous bytes of a row, then rows, then k) with
+// k-paired planes, or the R_CONTIG one (float4s along the rows of one k).
+template <int MODE, int ROWS>
+struct SlabPieces {
+    static constexpr int LD = MODE == K_CONTIG ? ROWS + 2 : ROWS + 4;
+    static constexpr int NU = ROWS * DB_BK / DB_THREADS / 4;
+    static constexpr int SZ = DB_BK * LD;
+    const uint8_t* src[NU];  // piece u of the part's first slab
+    int lo[NU];              // its LDS float offset
+    int64_t step;            // bytes from one slab to the next
+    f4 r[NU];
+
+    __device__ __forceinline__ void init(const uint8_t* base, int64_t nb_k, int64_t nb_r, int64_t row0, int64_t k0,
+                                         int tid) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int q = tid + DB_THREADS * u;
+            if constexpr (MODE == K_CONTIG) {
+                const int row = (q >> 2) % ROWS, kq = (q & 3) + 4 * (q / (4 * ROWS));
+                src[u] = base + (row0 + row) * nb_r + (k0 + 4 * kq) * 4;
+                lo[u] = (2 * kq) * 2 * LD + 2 * row;
+            } else {
+                const int k = q / (ROWS / 4), rq = q % (ROWS / 4);
+                src[u] = base + (row0 + 4 * rq) * 4 + (k0 + k) * nb_k;
+                lo[u] = k * LD + 4 * rq;
+            }
+        }
+        step = MODE == K_CONTIG ? (int64_t) DB_BK * 4 : (int64_t) DB_BK * nb_k;
+    }
+    __device__ __forceinline__ void load(int64_t s, int u) { r[u] = *(const f4*) (src[u] + s * step); }
+    __device__ __forceinline__ void store(float* l, int u) const {
+        if constexpr (MODE == K_CONTIG) {
+            *(float2*) (l + lo[u]) = float2{r[u].x, r[u].y};
+            *(float2*) (l + lo[u] + 2 * LD) = float2{r[u].z, r[u].w};
+        } else {
+            *(f4*) (l + lo[u]) = r[u];
+        }
+    }
+    // the k pair (k0, k0 + 1) of row r, k0 even
+    __device__ __forceinline__ static float2 pair(const float* l, int k0, int r) {
+        if constexpr (MODE == K_CONTIG) return *(const float2*) (l + (k0 >> 1) * 2 * LD + 2 * r);
+        else return float2{l[k0 * LD + r], l[(k0 + 1) * LD + r]};
+    }
+};
+
+template <int AMODE, int BMODE>
+__global__ __launch_bounds__(DB_THREADS) void k_mul_mat_db(MMArgs p) {
+    using PA = SlabPieces<AMODE, DB_BM>;
+    using PB = SlabPieces<BMODE, DB_BN>;
+    constexpr int NU = PA::NU + PB::NU;
+    static_assert(DB_L0 >= DB_S0, "a piece's registers are stored before the load of the slab after refills them");
+    static_assert(DB_S0 % 2 == 0 && DB_L0 % 2 == 0 && DB_S0 / 2 + NU <= DB_BK / 4 && DB_L0 / 2 + NU <= DB_BK / 4,
+                  "every piece is placed within the slab's k-steps");
+    __shared__ __attribute__((aligned(16))) float As[2][PA::SZ];
+    __shared__ __attribute__((aligned(16))) float Bs[2][PB::SZ];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wi = wave % DB_WI, wj = wave / DB_WI;
+    const int half = lane >> 5, col = lane & 31;
+
+    int64_t t = blockIdx.x;
+    if (p.xcd_planes) {
+        const int64_t tpp = p.tiles_i * p.tiles_j * 2, x = t & 7, k = t >> 3;
+        t = (8 * (k / tpp) + x) * tpp + k % tpp;
+    }
+    const int part = (int) (t & 1);
+    t >>= 1;
+    const int64_t tile = t;
+    const int64_t ti = t % p.tiles_i;
+    t /= p.tiles_i;
+    const int64_t tj = t % p.tiles_j;
+    const int64_t plane = t / p.tiles_j;
+    const int64_t i2 = plane % p.b_ne2, i3 = plane / p.b_ne2;
+    const uint8_t* a = p.a + (i2 % p.a_ne2) * p.a_nb2 + (i3 % p.a_ne3) * p.a_nb3;
+    const uint8_t* b = p.b + i2 * p.b_nb2 + i3 * p.b_nb3;
+    uint8_t* d = p.d + i2 * p.d_nb2 + i3 * p.d_nb3;
+    const int64_t i0 = ti * DB_BM, j0 = tj * DB_BN;
+    const int64_t nk = p.K / DB_BK / 2;  // slabs per part (K is a multiple of 2 DB_BK)
+    PA pa;
+    PB pb;
+    pa.init(a, p.a_nb0, p.a_nb1, i0, part * nk * DB_BK, tid);
+    pb.init(b, p.b_nb0, p.b_nb1, j0, part * nk * DB_BK, tid);
+    auto gload = [&](int64_t s, int u) {
+        if (u < PA::NU) pa.load(s, u);
+        else pb.load(s, u - PA::NU);
+    };
+    auto lstore = [&](int buf, int u) {
+        if (u < PA::NU) pa.store(As[buf], u);
+        else pb.store(Bs[buf], u - PA::NU);
+    };
+
+    f16v acc[DB_TI][DB_TJ];
+#pragma unroll
+    for (int x = 0; x < DB_TI; ++x)
+#pragma unroll
+        for (int y = 0; y < DB_TJ; ++y)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.f;
+    // slab 0 into buffer 0, slab 1 into the registers
+#pragma unroll
+    for (int u = 0; u < NU; ++u) gload(0, u);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) lstore(0, u);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) gload(1, u);
+    __syncthreads();
+
+    // slab kt from buffer kt % 2; STORE: the registers (slab kt + 1) go to the
+    // other buffer; LOAD: slab kt + 2 refills them. Compile-time flags keep the
+    // k-step loop one branch-free block.
+    auto slab = [&](int64_t kt, auto store_next, auto load_after) {
+        constexpr bool STORE = decltype(store_next)::value, LOAD = decltype(load_after)::value;
+        const int cur = (int) (kt & 1);
+        const float* ac = As[cur];
+        const float* bc = Bs[cur];
+#pragma unroll
+        for (int t4 = 0; t4 < DB_BK / 4; ++t4) {
+            const int k0 = 4 * t4 + 2 * half;
+            float2 av[DB_TI], bv[DB_TJ];
+#pragma unroll
+            for (int x = 0; x < DB_TI; ++x) av[x] = PA::pair(ac, k0, (wi * DB_TI + x) * 32 + col);
+#pragma unroll
+            for (int y = 0; y < DB_TJ; ++y) bv[y] = PB::pair(bc, k0, (wj * DB_TJ + y) * 32 + col);
+#pragma unroll
+            for (int x = 0; x < DB_TI; ++x)
+#pragma unroll
+                for (int y = 0; y < DB_TJ; ++y) {
+                    acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[y].x, av[x].x, acc[x][y], 0, 0, 0);
+                    acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[y].y, av[x].y, acc[x][y], 0, 0, 0);
+                }
+            if constexpr (STORE) {
+                if (t4 >= DB_S0 / 2 && t4 < DB_S0 / 2 + NU) lstore(cur ^ 1, t4 - DB_S0 / 2);
+            }
+            if constexpr (LOAD) {
+                if (t4 >= DB_L0 / 2 && t4 < DB_L0 / 2 + NU) gload(kt + 2, t4 - DB_L0 / 2);
+            }
+        }
+        __syncthreads();
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    // (nk >= 16 here; the guards also give the compiler the block layout that
+    // measured 146 us for dX against 149 us without them, the loop unchanged)
+    for (int64_t kt = 0; kt + 2 < nk; ++kt) slab(kt, yes{}, yes{});
+    if (nk >= 2) slab(nk - 2, yes{}, no{});
+    if (nk >= 1) slab(nk - 1, no{}, no{});
+
+    // the parts meet in dst (ticket_first and the protocol it begins, common.h)
+    auto out = [&](int x, int y, int v) -> float* {
+        const int64_t i = i0 + (wi * DB_TI + x) * 32 + col;
+        const int64_t j = j0 + (wj * DB_TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+        return i < p.M && j < p.N ? (float*) (d + i * p.d_nb0 + j * p.d_nb1) : nullptr;
+    };
+    uint32_t* tk = p.tickets + 2 * (tile * (DB_WI * DB_WJ) + wave);
+    if (ticket_first(tk, lane)) {
+#pragma unroll
+        for (int x = 0; x < DB_TI; ++x)
+#pragma unroll
+            for (int y = 0; y < DB_TJ; ++y)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    if (float* o = out(x, y, v))
+                        __hip_atomic_store(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ticket_publish(tk, lane);
+        return;
+    }
+    ticket_wait(tk, lane);
+#pragma unroll
+    for (int x = 0; x < DB_TI; ++x)
+#pragma unroll
+        for (int y = 0; y < DB_TJ; ++y)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                if (float* o = out(x, y, v))
+                    __hip_atomic_fetch_add(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket_clear(tk, lane);
+}
+
 // ---------------------------------------------------------------- few columns
 //
 // dst = W . X with N <= 64 columns and W k-contiguous (the weight of a Linear
@@ -744,6 +948,22 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
         static_assert(511 * 8 * 2 <= MM_TICKETS, "two ticket words per wave of under 512 tiles");
         const int rc = mm_stream_tickets(stream, &p.tickets);
         if (rc != TRC_HIP_OK) return rc;
+        // whole tiles and slabs with float4 loaders: double-buffered slabs
+        if (p.M % DB_BM == 0 && p.N % DB_BN == 0 && p.K % (2 * DB_BK) == 0 && am != GENERIC && bm != GENERIC) {
+            p.tiles_i = p.M / DB_BM;
+            p.tiles_j = p.N / DB_BN;
+            p.xcd_planes = planes % 8 == 0 ? 1 : 0;
+            p.d_span = (p.M - 1) * p.d_nb0 + (p.N - 1) * p.d_nb1 + 4;
+            const int64_t grid = p.tiles_i * p.tiles_j * planes * 2;
+#define TRC_MM_DB(A, B) \
+    if (am == A && bm == B) hipLaunchKernelGGL((k_mul_mat_db<A, B>), dim3((unsigned) grid), dim3(DB_THREADS), 0, stream, p);
+            TRC_MM_DB(K_CONTIG, K_CONTIG)
+            TRC_MM_DB(K_CONTIG, R_CONTIG)
+            TRC_MM_DB(R_CONTIG, K_CONTIG)
+            TRC_MM_DB(R_CONTIG, R_CONTIG)
+#undef TRC_MM_DB
+            return check_launch("mul_mat_f32 (K in two parts, whole tiles)");
+        }
         // a transposed src0 against a k-contiguous src1 (the dX product of a
         // Linear layer): k-paired LDS planes for src1, 4 % faster there; 1.5 %
         // slower with both operands k-contiguous (the forward product)
