@@ -417,36 +417,57 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
     }
 }
 
-// ------------------------------------------------ K split in two, whole tiles
+// ------------------------------------------ double-buffered slabs, whole tiles
 //
-// The products whose K is split in two (one 8-wave workgroup per CU for a
-// 128 x 128 tile and half of K), when every tile and slab is whole (M and N
-// multiples of 128, K of 64) and both operands load as float4s (k- or
-// row-contiguous). k_mul_mat stores each slab between two barriers while no
-// MFMA runs; here two LDS slab buffers take turns: during the MFMAs of slab s
-// the registers holding slab s + 1 are stored into the other buffer (from
-// k-step DB_S0 on, one float4 per k-step) and then refilled with slab s + 2
-// (from k-step DB_L0 on), with one barrier per slab. Whole tiles need no bounds
-// checks, which keeps the slab loop free of branches and selects (with
-// clamped addresses and selects the same schedule measured 157-160 us, slower
-// than k_mul_mat). Both operands are read as k-paired LDS planes where they
-// are k-contiguous, so the MFMAs take k in groups of 4 (k = 4t + 2 half, then
-// 4t + 2 half + 1). Configuration 3 (interleaved minimums, one box): forward
-// 149.5 -> 139.5 us (its sums now group k by pairs, within 6e-5 of 281), dX
-// 148.8 -> 146.0 us (same bits). The two parts meet in dst through the
-// stream's ticket words as in k_mul_mat.
-constexpr int DB_WI = 2, DB_WJ = 4, DB_TI = 2, DB_TJ = 1, DB_BK = 32, DB_S0 = 2, DB_L0 = 8;
+// 128 x 128 tiles on 8-wave workgroups (64 x 32 per wave) when every tile and
+// slab is whole (M and N multiples of 128, K of 2 slabs per part) and both
+// operands load as float4s (k- or row-contiguous). k_mul_mat stores each slab
+// between two barriers while no MFMA runs, with both waves of every SIMD
+// waiting together; here two LDS slab buffers take turns: during the MFMAs of
+// slab s the registers holding slab s + 1 are stored into the idle buffer (one
+// float4 piece per group of 4 k, from group S0 on) and then refilled with slab
+// s + 2 (from group L0 on), with one barrier per slab. Whole tiles need no
+// bounds checks, which keeps the slab loop free of branches and selects (with
+// clamped addresses and selects the split schedule measured 157-160 us, slower
+// than k_mul_mat). Both operands are read as k-paired LDS planes where they are
+// k-contiguous, so the MFMAs take k in groups of 4 (k = 4t + 2 half, then
+// 4t + 2 half + 1). Two uses (interleaved minimums, one box, configuration 3 /
+// 4):
+//   - K split in two (DbPlan<2>: 32-deep slabs, default priority), the parts
+//     meeting in dst through the stream's ticket words as in k_mul_mat:
+//     forward 149.5 -> 139.5 us (its sums now group k by pairs, within 6e-5 of
+//     281), dX 148.8 -> 146.0 us (same bits);
+//   - K whole (DbPlan<1>: 16-deep slabs, two workgroups per CU, the MFMA-block
+//     priority of k_mul_mat): dW 135.3 -> 129.7 us, configuration 4 158.5 ->
+//     147.2 us; ACC adds the product into dst as k_mul_mat's ACC does.
+constexpr int DB_WI = 2, DB_WJ = 4, DB_TI = 2, DB_TJ = 1;
 constexpr int DB_THREADS = DB_WI * DB_WJ * 64;
 constexpr int DB_BM = DB_WI * DB_TI * 32, DB_BN = DB_WJ * DB_TJ * 32;
+// slab depth, the group of 4 k from which a slab's pieces are stored (S0) and
+// the next slab's loaded (L0), and the MFMA-block priority, per number of K parts
+template <int SPLIT>
+struct DbPlan;
+template <>
+struct DbPlan<2> {
+    static constexpr int BK = 32, S0 = 1, L0 = 4;
+    static constexpr bool PRIO = false;
+};
+template <>
+struct DbPlan<1> {
+    static constexpr int BK = 16, S0 = 0, L0 = 1;
+    static constexpr bool PRIO = true;
+};
 
 // One operand's slab as NU float4 pieces per thread: the K_CONTIG mapping of
 // SlabLoader (4 lanes per 64 contiguous bytes of a row, then rows, then k) with
 // k-paired planes, or the R_CONTIG one (float4s along the rows of one k).
-template <int MODE, int ROWS>
+template <int MODE, int ROWS, int BK>
 struct SlabPieces {
+    static_assert(MODE != K_CONTIG || BK % 16 == 0, "k-contiguous pieces come in 16-k groups");
+    static_assert(ROWS * BK % (DB_THREADS * 4) == 0, "whole float4 pieces per thread");
     static constexpr int LD = MODE == K_CONTIG ? ROWS + 2 : ROWS + 4;
-    static constexpr int NU = ROWS * DB_BK / DB_THREADS / 4;
-    static constexpr int SZ = DB_BK * LD;
+    static constexpr int NU = ROWS * BK / DB_THREADS / 4;
+    static constexpr int SZ = BK * LD;
     const uint8_t* src[NU];  // piece u of the part's first slab
     int lo[NU];              // its LDS float offset
     int64_t step;            // bytes from one slab to the next
@@ -467,7 +488,7 @@ struct SlabPieces {
                 lo[u] = k * LD + 4 * rq;
             }
         }
-        step = MODE == K_CONTIG ? (int64_t) DB_BK * 4 : (int64_t) DB_BK * nb_k;
+        step = MODE == K_CONTIG ? (int64_t) BK * 4 : (int64_t) BK * nb_k;
     }
     __device__ __forceinline__ void load(int64_t s, int u) { r[u] = *(const f4*) (src[u] + s * step); }
     __device__ __forceinline__ void store(float* l, int u) const {
@@ -485,14 +506,16 @@ struct SlabPieces {
     }
 };
 
-template <int AMODE, int BMODE>
+template <int AMODE, int BMODE, int SPLIT, bool ACC = false>
 __global__ __launch_bounds__(DB_THREADS) void k_mul_mat_db(MMArgs p) {
-    using PA = SlabPieces<AMODE, DB_BM>;
-    using PB = SlabPieces<BMODE, DB_BN>;
+    using PL = DbPlan<SPLIT>;
+    constexpr int BK = PL::BK;
+    using PA = SlabPieces<AMODE, DB_BM, BK>;
+    using PB = SlabPieces<BMODE, DB_BN, BK>;
     constexpr int NU = PA::NU + PB::NU;
-    static_assert(DB_L0 >= DB_S0, "a piece's registers are stored before the load of the slab after refills them");
-    static_assert(DB_S0 % 2 == 0 && DB_L0 % 2 == 0 && DB_S0 / 2 + NU <= DB_BK / 4 && DB_L0 / 2 + NU <= DB_BK / 4,
-                  "every piece is placed within the slab's k-steps");
+    static_assert(!ACC || SPLIT == 1, "d + a + b would round differently from d + (a + b)");
+    static_assert(PL::L0 >= PL::S0, "a piece's registers are stored before the load of the slab after refills them");
+    static_assert(PL::S0 + NU <= BK / 4 && PL::L0 + NU <= BK / 4, "every piece is placed within the slab's k groups");
     __shared__ __attribute__((aligned(16))) float As[2][PA::SZ];
     __shared__ __attribute__((aligned(16))) float Bs[2][PB::SZ];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -501,11 +524,11 @@ __global__ __launch_bounds__(DB_THREADS) void k_mul_mat_db(MMArgs p) {
 
     int64_t t = blockIdx.x;
     if (p.xcd_planes) {
-        const int64_t tpp = p.tiles_i * p.tiles_j * 2, x = t & 7, k = t >> 3;
+        const int64_t tpp = p.tiles_i * p.tiles_j * SPLIT, x = t & 7, k = t >> 3;
         t = (8 * (k / tpp) + x) * tpp + k % tpp;
     }
-    const int part = (int) (t & 1);
-    t >>= 1;
+    const int part = SPLIT > 1 ? (int) (t % SPLIT) : 0;
+    t /= SPLIT;
     const int64_t tile = t;
     const int64_t ti = t % p.tiles_i;
     t /= p.tiles_i;
@@ -516,11 +539,11 @@ __global__ __launch_bounds__(DB_THREADS) void k_mul_mat_db(MMArgs p) {
     const uint8_t* b = p.b + i2 * p.b_nb2 + i3 * p.b_nb3;
     uint8_t* d = p.d + i2 * p.d_nb2 + i3 * p.d_nb3;
     const int64_t i0 = ti * DB_BM, j0 = tj * DB_BN;
-    const int64_t nk = p.K / DB_BK / 2;  // slabs per part (K is a multiple of 2 DB_BK)
+    const int64_t nk = p.K / BK / SPLIT;  // slabs per part (at least 2)
     PA pa;
     PB pb;
-    pa.init(a, p.a_nb0, p.a_nb1, i0, part * nk * DB_BK, tid);
-    pb.init(b, p.b_nb0, p.b_nb1, j0, part * nk * DB_BK, tid);
+    pa.init(a, p.a_nb0, p.a_nb1, i0, part * nk * BK, tid);
+    pb.init(b, p.b_nb0, p.b_nb1, j0, part * nk * BK, tid);
     auto gload = [&](int64_t s, int u) {
         if (u < PA::NU) pa.load(s, u);
         else pb.load(s, u - PA::NU);
@@ -548,14 +571,15 @@ __global__ __launch_bounds__(DB_THREADS) void k_mul_mat_db(MMArgs p) {
 
     // slab kt from buffer kt % 2; STORE: the registers (slab kt + 1) go to the
     // other buffer; LOAD: slab kt + 2 refills them. Compile-time flags keep the
-    // k-step loop one branch-free block.
+    // k loop one branch-free block.
     auto slab = [&](int64_t kt, auto store_next, auto load_after) {
         constexpr bool STORE = decltype(store_next)::value, LOAD = decltype(load_after)::value;
         const int cur = (int) (kt & 1);
         const float* ac = As[cur];
         const float* bc = Bs[cur];
+        if constexpr (PL::PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int t4 = 0; t4 < DB_BK / 4; ++t4) {
+        for (int t4 = 0; t4 < BK / 4; ++t4) {
             const int k0 = 4 * t4 + 2 * half;
             float2 av[DB_TI], bv[DB_TJ];
 #pragma unroll
@@ -570,30 +594,46 @@ __global__ __launch_bounds__(DB_THREADS) void k_mul_mat_db(MMArgs p) {
                     acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[y].y, av[x].y, acc[x][y], 0, 0, 0);
                 }
             if constexpr (STORE) {
-                if (t4 >= DB_S0 / 2 && t4 < DB_S0 / 2 + NU) lstore(cur ^ 1, t4 - DB_S0 / 2);
+                if (t4 >= PL::S0 && t4 < PL::S0 + NU) lstore(cur ^ 1, t4 - PL::S0);
             }
             if constexpr (LOAD) {
-                if (t4 >= DB_L0 / 2 && t4 < DB_L0 / 2 + NU) gload(kt + 2, t4 - DB_L0 / 2);
+                if (t4 >= PL::L0 && t4 < PL::L0 + NU) gload(kt + 2, t4 - PL::L0);
             }
         }
+        if constexpr (PL::PRIO) __builtin_amdgcn_s_setprio(0);
         __syncthreads();
     };
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
-    // (nk >= 16 here; the guards also give the compiler the block layout that
+    // (nk >= 2 here; the guards also give the compiler the block layout that
     // measured 146 us for dX against 149 us without them, the loop unchanged)
     for (int64_t kt = 0; kt + 2 < nk; ++kt) slab(kt, yes{}, yes{});
     if (nk >= 2) slab(nk - 2, yes{}, no{});
     if (nk >= 1) slab(nk - 1, no{}, no{});
 
-    // the parts meet in dst (ticket_first and the protocol it begins, common.h)
+    // accumulator register v of tile (x, y) holds dst row i = i0 + (wi TI + x) 32
+    // + col and column j = j0 + (wj TJ + y) 32 + 8 (v / 4) + 4 half + v % 4
     auto out = [&](int x, int y, int v) -> float* {
         const int64_t i = i0 + (wi * DB_TI + x) * 32 + col;
         const int64_t j = j0 + (wj * DB_TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
         return i < p.M && j < p.N ? (float*) (d + i * p.d_nb0 + j * p.d_nb1) : nullptr;
     };
-    uint32_t* tk = p.tickets + 2 * (tile * (DB_WI * DB_WJ) + wave);
-    if (ticket_first(tk, lane)) {
+    if constexpr (SPLIT > 1) {
+        // the parts meet in dst (ticket_first and the protocol it begins, common.h)
+        uint32_t* tk = p.tickets + 2 * (tile * (DB_WI * DB_WJ) + wave);
+        if (ticket_first(tk, lane)) {
+#pragma unroll
+            for (int x = 0; x < DB_TI; ++x)
+#pragma unroll
+                for (int y = 0; y < DB_TJ; ++y)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        if (float* o = out(x, y, v))
+                            __hip_atomic_store(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ticket_publish(tk, lane);
+            return;
+        }
+        ticket_wait(tk, lane);
 #pragma unroll
         for (int x = 0; x < DB_TI; ++x)
 #pragma unroll
@@ -601,20 +641,77 @@ __global__ __launch_bounds__(DB_THREADS) void k_mul_mat_db(MMArgs p) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v)
                     if (float* o = out(x, y, v))
-                        __hip_atomic_store(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ticket_publish(tk, lane);
-        return;
+                        __hip_atomic_fetch_add(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ticket_clear(tk, lane);
+    } else if constexpr (ACC) {
+        // d + v, one 32 x 32 block at a time with its 16 old values read before
+        // any store, through a buffer resource over the dst plane (as k_mul_mat's
+        // ACC epilogue; the tile is whole, so one lane offset and uniform
+        // multiples of nb1 address all 16)
+        const __amdgpu_buffer_rsrc_t rd =
+            __builtin_amdgcn_make_buffer_rsrc((void*) d, (short) 0, (int) p.d_span, MM_RSRC_WORD3);
+#pragma unroll
+        for (int x = 0; x < DB_TI; ++x) {
+            const int64_t i = i0 + (wi * DB_TI + x) * 32 + col;
+#pragma unroll
+            for (int y = 0; y < DB_TJ; ++y) {
+                const int64_t jb = j0 + (wj * DB_TJ + y) * 32 + 4 * half;
+                const uint32_t vo = (uint32_t) (i * p.d_nb0 + jb * p.d_nb1);
+                float old[16];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const uint32_t so = (uint32_t) ((8 * (v >> 2) + (v & 3)) * p.d_nb1);
+                    old[v] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, vo, so, 0));
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const uint32_t so = (uint32_t) ((8 * (v >> 2) + (v & 3)) * p.d_nb1);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, old[v] + acc[x][y][v]), rd, vo,
+                                                          so, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    } else {
+        // non-temporal: dst is not read again by this launch. The tile is
+        // whole, so no element needs a bounds check; with out()'s check (and
+        // its branches) dW took 145-148 us instead of 131
+#pragma unroll
+        for (int x = 0; x < DB_TI; ++x)
+#pragma unroll
+            for (int y = 0; y < DB_TJ; ++y)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t i = i0 + (wi * DB_TI + x) * 32 + col;
+                    const int64_t j = j0 + (wj * DB_TJ + y) * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                    __builtin_nontemporal_store(acc[x][y][v], (float*) (d + i * p.d_nb0 + j * p.d_nb1));
+                }
     }
-    ticket_wait(tk, lane);
-#pragma unroll
-    for (int x = 0; x < DB_TI; ++x)
-#pragma unroll
-        for (int y = 0; y < DB_TJ; ++y)
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                if (float* o = out(x, y, v))
-                    __hip_atomic_fetch_add(o, acc[x][y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ticket_clear(tk, lane);
+}
+
+// Launches k_mul_mat_db when the shape fits it (whole tiles and slabs, float4
+// loaders, the K parts' ticket words in p.tickets when SPLIT is 2); returns
+// -1 (launching nothing) otherwise.
+template <int SPLIT, bool ACC>
+int launch_db(MMArgs& p, int am, int bm, int64_t planes, hipStream_t stream) {
+    constexpr int BK = DbPlan<SPLIT>::BK;
+    if (p.M % DB_BM != 0 || p.N % DB_BN != 0 || p.K % (2 * BK * SPLIT) != 0 || am == GENERIC || bm == GENERIC)
+        return -1;
+    p.tiles_i = p.M / DB_BM;
+    p.tiles_j = p.N / DB_BN;
+    p.xcd_planes = planes % 8 == 0 ? 1 : 0;
+    p.d_span = (p.M - 1) * p.d_nb0 + (p.N - 1) * p.d_nb1 + 4;
+    const int64_t grid = p.tiles_i * p.tiles_j * planes * SPLIT;
+    if (grid > 0x7FFFFFFF) return fail(TRC_HIP_E_SHAPE, "mul_mat: %lld workgroups exceed one launch", (long long) grid);
+#define TRC_MM_DB(A, B) \
+    if (am == A && bm == B) \
+        hipLaunchKernelGGL((k_mul_mat_db<A, B, SPLIT, ACC>), dim3((unsigned) grid), dim3(DB_THREADS), 0, stream, p);
+    TRC_MM_DB(K_CONTIG, K_CONTIG)
+    TRC_MM_DB(K_CONTIG, R_CONTIG)
+    TRC_MM_DB(R_CONTIG, K_CONTIG)
+    TRC_MM_DB(R_CONTIG, R_CONTIG)
+#undef TRC_MM_DB
+    return check_launch("mul_mat_f32 (double-buffered slabs)");
 }
 
 // ---------------------------------------------------------------- few columns
@@ -937,11 +1034,20 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
     // stream's workspace); otherwise 64x64 tiles.
     const int64_t big_tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128) * planes;
     if (accumulate) {
-        // K stays in one part: the large tiles when they fill the CUs twice, else 64 x 64
-        if (big_tiles >= 512) return dispatch_modes<2, 2, 2, 2, 16, 1, true>(p, am, bm, planes, stream);
+        // K stays in one part: the large tiles when they fill the CUs twice
+        // (double-buffered when whole), else 64 x 64
+        if (big_tiles >= 512) {
+            const int drc = launch_db<1, true>(p, am, bm, planes, stream);
+            if (drc >= 0) return drc;
+            return dispatch_modes<2, 2, 2, 2, 16, 1, true>(p, am, bm, planes, stream);
+        }
         return dispatch_modes<2, 2, 1, 1, 32, 1, true>(p, am, bm, planes, stream);
     }
-    if (big_tiles >= 512) return dispatch_modes<2, 2, 2, 2, 16, 1>(p, am, bm, planes, stream);
+    if (big_tiles >= 512) {
+        const int drc = launch_db<1, false>(p, am, bm, planes, stream);
+        if (drc >= 0) return drc;
+        return dispatch_modes<2, 2, 2, 2, 16, 1>(p, am, bm, planes, stream);
+    }
     const bool dense_dst = p.d_nb0 == 4 && p.d_nb1 == 4 * p.M && p.d_nb2 == p.d_nb1 * p.N &&
                            p.d_nb3 == p.d_nb2 * b.ne[2];
     if (dense_dst && p.K >= 1024 && 2 * big_tiles >= device_cus()) {
@@ -949,21 +1055,8 @@ int launch_mul_mat_f32(const trc_hip_tensor& a, const trc_hip_tensor& b, const t
         const int rc = mm_stream_tickets(stream, &p.tickets);
         if (rc != TRC_HIP_OK) return rc;
         // whole tiles and slabs with float4 loaders: double-buffered slabs
-        if (p.M % DB_BM == 0 && p.N % DB_BN == 0 && p.K % (2 * DB_BK) == 0 && am != GENERIC && bm != GENERIC) {
-            p.tiles_i = p.M / DB_BM;
-            p.tiles_j = p.N / DB_BN;
-            p.xcd_planes = planes % 8 == 0 ? 1 : 0;
-            p.d_span = (p.M - 1) * p.d_nb0 + (p.N - 1) * p.d_nb1 + 4;
-            const int64_t grid = p.tiles_i * p.tiles_j * planes * 2;
-#define TRC_MM_DB(A, B) \
-    if (am == A && bm == B) hipLaunchKernelGGL((k_mul_mat_db<A, B>), dim3((unsigned) grid), dim3(DB_THREADS), 0, stream, p);
-            TRC_MM_DB(K_CONTIG, K_CONTIG)
-            TRC_MM_DB(K_CONTIG, R_CONTIG)
-            TRC_MM_DB(R_CONTIG, K_CONTIG)
-            TRC_MM_DB(R_CONTIG, R_CONTIG)
-#undef TRC_MM_DB
-            return check_launch("mul_mat_f32 (K in two parts, whole tiles)");
-        }
+        const int drc = launch_db<2, false>(p, am, bm, planes, stream);
+        if (drc >= 0) return drc;
         // a transposed src0 against a k-contiguous src1 (the dX product of a
         // Linear layer): k-paired LDS planes for src1, 4 % faster there; 1.5 %
         // slower with both operands k-contiguous (the forward product)
