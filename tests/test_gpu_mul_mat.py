@@ -112,6 +112,8 @@ def test_backward_goldens(hip, case):
     # the same with whole tiles and slabs (double-buffered slabs): broadcast
     # planes, and 8 planes (each plane's tiles on one XCD)
     (1024, 1024, 512, 4, 1, 2, 1), (1088, 512, 512, 8, 1, 1, 1),
+    # 512 or more whole 128x128 tiles, K whole (double-buffered slabs)
+    (64, 4096, 2048, 1, 1, 1, 1),
     # plane counts that are a multiple of 8 (each plane's tiles on one XCD):
     # ragged 64x64 tiles over 8 planes, ragged 128x128 tiles over 64 planes
     (33, 70, 90, 4, 2, 1, 1), (40, 300, 300, 8, 8, 1, 1),
@@ -395,6 +397,8 @@ def _acc_run(A, a_view_fn, B, b_view_fn, D0):
     # products, and the few-column kernel
     (512, 4096, 4096, True, True), (128, 1024, 768, True, True), (300, 130, 70, False, True),
     (4096, 4096, 8, False, False), (1000, 77, 7, False, False), (96, 48, 40, True, False),
+    # 512 whole tiles with k-contiguous operands (double-buffered slabs)
+    (256, 4096, 2048, False, False), (64, 4096, 2048, False, True), (96, 4096, 2048, True, False),
 ])
 def test_mul_mat_acc_adds_the_product(hip, shape):
     """Each element gets the product's float sum, then one float add into dst: the
