@@ -433,27 +433,32 @@ __global__ __launch_bounds__(WI * WJ * 64) void k_mul_mat(MMArgs p) {
 // k-contiguous, so the MFMAs take k in groups of 4 (k = 4t + 2 half, then
 // 4t + 2 half + 1). Two uses (interleaved minimums, one box, configuration 3 /
 // 4):
-//   - K split in two (DbPlan<2>: 32-deep slabs, default priority), the parts
-//     meeting in dst through the stream's ticket words as in k_mul_mat:
-//     forward 149.5 -> 139.5 us (its sums now group k by pairs, within 6e-5 of
+//   - K split in two (DbPlan<2, ...>: 32-deep slabs, default priority), the
+//     parts meeting in dst through the stream's ticket words as in k_mul_mat:
+//     forward 149.5 -> 137.4 us (its sums now group k by pairs, within 6e-5 of
 //     281), dX 148.8 -> 146.0 us (same bits);
-//   - K whole (DbPlan<1>: 16-deep slabs, two workgroups per CU, the MFMA-block
+//   - K whole (DbPlan<1, ...>: 16-deep slabs, two workgroups per CU, the MFMA-block
 //     priority of k_mul_mat): dW 135.3 -> 129.7 us, configuration 4 158.5 ->
 //     147.2 us; ACC adds the product into dst as k_mul_mat's ACC does.
 constexpr int DB_WI = 2, DB_WJ = 4, DB_TI = 2, DB_TJ = 1;
 constexpr int DB_THREADS = DB_WI * DB_WJ * 64;
 constexpr int DB_BM = DB_WI * DB_TI * 32, DB_BN = DB_WJ * DB_TJ * 32;
 // slab depth, the group of 4 k from which a slab's pieces are stored (S0) and
-// the next slab's loaded (L0), and the MFMA-block priority, per number of K parts
-template <int SPLIT>
+// the next slab's loaded (L0), and the MFMA-block priority, per number of K
+// parts and src0 layout. Measured on configuration 3 (µs): the forward product
+// (k-contiguous src0) 140.0 with S0 = 1, 137.3-137.5 with S0 = 0 and L0 = 1..4;
+// dX (row-contiguous src0) 146.0-146.2 with S0 = 1 and L0 = 3..4, 146.9-149.9
+// with S0 = 0 or 2; the priority made both slower (141.0, 153.3), 64-deep slabs
+// changed them by under 1 %.
+template <int SPLIT, int AMODE>
 struct DbPlan;
-template <>
-struct DbPlan<2> {
-    static constexpr int BK = 32, S0 = 1, L0 = 4;
+template <int AMODE>
+struct DbPlan<2, AMODE> {
+    static constexpr int BK = 32, S0 = AMODE == K_CONTIG ? 0 : 1, L0 = AMODE == K_CONTIG ? 2 : 4;
     static constexpr bool PRIO = false;
 };
-template <>
-struct DbPlan<1> {
+template <int AMODE>
+struct DbPlan<1, AMODE> {
     static constexpr int BK = 16, S0 = 0, L0 = 1;
     static constexpr bool PRIO = true;
 };
@@ -508,7 +513,7 @@ struct SlabPieces {
 
 template <int AMODE, int BMODE, int SPLIT, bool ACC = false>
 __global__ __launch_bounds__(DB_THREADS) void k_mul_mat_db(MMArgs p) {
-    using PL = DbPlan<SPLIT>;
+    using PL = DbPlan<SPLIT, AMODE>;
     constexpr int BK = PL::BK;
     using PA = SlabPieces<AMODE, DB_BM, BK>;
     using PB = SlabPieces<BMODE, DB_BN, BK>;
@@ -694,7 +699,8 @@ __global__ __launch_bounds__(DB_THREADS) void k_mul_mat_db(MMArgs p) {
 // -1 (launching nothing) otherwise.
 template <int SPLIT, bool ACC>
 int launch_db(MMArgs& p, int am, int bm, int64_t planes, hipStream_t stream) {
-    constexpr int BK = DbPlan<SPLIT>::BK;
+    static_assert(DbPlan<SPLIT, K_CONTIG>::BK == DbPlan<SPLIT, R_CONTIG>::BK, "one slab depth per K split");
+    constexpr int BK = DbPlan<SPLIT, K_CONTIG>::BK;
     if (p.M % DB_BM != 0 || p.N % DB_BN != 0 || p.K % (2 * BK * SPLIT) != 0 || am == GENERIC || bm == GENERIC)
         return -1;
     p.tiles_i = p.M / DB_BM;
