@@ -706,7 +706,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; multi-GPU runs are not part of this "
-                                   "build (the sharding design is in DESIGN.md)", "n_gpus": args.gpus}))
+                                   "build (sharding across GPUs is designed, not built)", "n_gpus": args.gpus}))
         sys.exit(2)
 
     pkg = load_pkg()
