@@ -234,18 +234,23 @@ __global__ __launch_bounds__(SR_THREADS) void k_sum_rows(const uint8_t* __restri
 // SB_D chunks of SB_C floats per row, loaded by all SB_THREADS threads (1 KB
 // runs per row) SB_D - 1 chunks ahead of the lanes that hold the rows' sums;
 // lane r of wave 0 adds row r's chunk in element order. With SB_D >= 3 one
-// barrier per chunk separates a slot's reads from its next fill.
+// barrier per chunk separates a slot's reads from its next fill. The threads
+// that stage a chunk convert it to double (exact) as they store it, so the
+// lanes on the chain issue only the adds (configuration 3's loss: 29.1 ->
+// 27.0 us per launch). What remains is the chain itself: each dependent
+// v_add_f64 waits ~15 cycles for the one before, 4096 of them per row.
 constexpr int SB_ROWS = 8;
 constexpr int SB_THREADS = 256;
 constexpr int SB_C = 256;
-constexpr int SB_LD = SB_C + 4;  // padded row (in floats) of an LDS slot
+constexpr int SB_LD = SB_C + 2;  // padded row (in doubles) of an LDS slot: rows 4 banks apart
+typedef double sb_d2 __attribute__((ext_vector_type(2)));
 constexpr int SB_D = 4;
 constexpr int SB_PER = SB_ROWS * SB_C / 4 / SB_THREADS;  // float4 loads per thread and chunk
 static_assert(SB_PER * SB_THREADS * 4 == SB_ROWS * SB_C, "a chunk is whole float4s per thread");
 
 __global__ __launch_bounds__(SB_THREADS) void k_sum_rows_lds(const uint8_t* __restrict__ a, Shape4 sa,
                                                              double* __restrict__ part) {
-    __shared__ __attribute__((aligned(16))) float ring[SB_D * SB_ROWS * SB_LD];
+    __shared__ __attribute__((aligned(16))) double ring[SB_D * SB_ROWS * SB_LD];
     const int64_t rows = sa.ne[1] * sa.ne[2] * sa.ne[3];
     const int64_t r0 = (int64_t) blockIdx.x * SB_ROWS;
     const int64_t n = sa.ne[0];
@@ -275,9 +280,13 @@ __global__ __launch_bounds__(SB_THREADS) void k_sum_rows_lds(const uint8_t* __re
         }
     };
     auto store = [&](int64_t c, const f4 (&v)[SB_PER]) {
-        float* slot = ring + (int) (c % SB_D) * SB_ROWS * SB_LD;
+        double* slot = ring + (int) (c % SB_D) * SB_ROWS * SB_LD;
 #pragma unroll
-        for (int u = 0; u < SB_PER; ++u) *(f4*) (slot + lrow[u] * SB_LD + 4 * lq[u]) = v[u];
+        for (int u = 0; u < SB_PER; ++u) {
+            double* dst = slot + lrow[u] * SB_LD + 4 * lq[u];
+            *(sb_d2*) dst = sb_d2{(double) v[u].x, (double) v[u].y};
+            *(sb_d2*) (dst + 2) = sb_d2{(double) v[u].z, (double) v[u].w};
+        }
     };
     for (int64_t c = 0; c < SB_D - 1 && c < chunks; ++c) {
         f4 v[SB_PER];
@@ -292,33 +301,31 @@ __global__ __launch_bounds__(SB_THREADS) void k_sum_rows_lds(const uint8_t* __re
         const bool more = c + SB_D - 1 < chunks;
         if (more) load(c + SB_D - 1, v);
         if (chain) {
-            const float* row = ring + (int) (c % SB_D) * SB_ROWS * SB_LD + tid * SB_LD;
+            const double* row = ring + (int) (c % SB_D) * SB_ROWS * SB_LD + tid * SB_LD;
             const int64_t m = n - c * SB_C < SB_C ? n - c * SB_C : SB_C;
             if (m == SB_C) {
-                // a whole chunk: the next 16 floats are read from LDS while the
+                // a whole chunk: the next 16 values are read from LDS while the
                 // current 16 are added, so only the adds stay on the chain
-                const f4* row4 = (const f4*) row;
-                f4 cur[4], nxt[4];
+                const sb_d2* row2 = (const sb_d2*) row;
+                sb_d2 cur[8], nxt[8];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) cur[k] = row4[k];
+                for (int k = 0; k < 8; ++k) cur[k] = row2[k];
 #pragma unroll
                 for (int g = 0; g < SB_C / 16; ++g) {
                     if (g + 1 < SB_C / 16) {
 #pragma unroll
-                        for (int k = 0; k < 4; ++k) nxt[k] = row4[4 * (g + 1) + k];
+                        for (int k = 0; k < 8; ++k) nxt[k] = row2[8 * (g + 1) + k];
                     }
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        s = s + (double) cur[k].x;
-                        s = s + (double) cur[k].y;
-                        s = s + (double) cur[k].z;
-                        s = s + (double) cur[k].w;
+                    for (int k = 0; k < 8; ++k) {
+                        s = s + cur[k].x;
+                        s = s + cur[k].y;
                     }
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) cur[k] = nxt[k];
+                    for (int k = 0; k < 8; ++k) cur[k] = nxt[k];
                 }
             } else {
-                for (int64_t i = 0; i < m; ++i) s = s + (double) row[i];
+                for (int64_t i = 0; i < m; ++i) s = s + row[i];
             }
         }
         __syncthreads();
